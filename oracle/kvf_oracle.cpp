@@ -1,0 +1,395 @@
+// kvf_oracle.cpp - CPU restatement of KVForge's host-side arithmetic.
+//
+// TEST INFRASTRUCTURE ONLY: the checker for the HIP path. Built with
+// -ffp-contract=off so that no multiply-add is fused, as in the reference's
+// host code. Reference citations are given per function in kvf_oracle.h.
+#include "kvf_oracle.h"
+
+#include <algorithm>
+#include <cmath>
+#include <cstring>
+#include <limits>
+#include <numeric>
+#include <random>
+#include <vector>
+
+namespace {
+
+// IEEE binary16 from binary32, round to nearest, ties to even. Written from
+// the format definition (1 sign, 5 exponent bits with bias 15, 10 fraction
+// bits; subnormal unit 2^-24).
+uint16_t f2h(float f) {
+  uint32_t x;
+  std::memcpy(&x, &f, 4);
+  const uint32_t sign = (x >> 16) & 0x8000u;
+  const uint32_t ax = x & 0x7fffffffu;
+  if (ax >= 0x7f800000u) // inf, nan
+    return (uint16_t)(sign | 0x7c00u | (ax > 0x7f800000u ? 0x200u | ((ax >> 13) & 0x3ffu) : 0u));
+  if (ax >= 0x38800000u) { // |f| >= 2^-14: normal half (or overflow)
+    const uint32_t e = (ax >> 23) - 112u; // rebias 127 -> 15
+    if (e >= 31u)
+      return (uint16_t)(sign | 0x7c00u);
+    uint32_t h = (e << 10) | ((ax >> 13) & 0x3ffu);
+    const uint32_t rem = ax & 0x1fffu;
+    if (rem > 0x1000u || (rem == 0x1000u && (h & 1u)))
+      ++h; // a carry out of the fraction bumps the exponent, up to inf
+    return (uint16_t)(sign | h);
+  }
+  if (ax < 0x33000000u) // below 2^-25: rounds to zero
+    return (uint16_t)sign;
+  const uint32_t e = ax >> 23;
+  const uint32_t mant = (ax & 0x7fffffu) | 0x800000u;
+  const uint32_t shift = 126u - e; // value / 2^-24 = mant * 2^(e-126)
+  uint32_t h = mant >> shift;
+  const uint32_t rem = mant & ((1u << shift) - 1u);
+  const uint32_t half = 1u << (shift - 1u);
+  if (rem > half || (rem == half && (h & 1u)))
+    ++h;
+  return (uint16_t)(sign | h);
+}
+
+float h2f(uint16_t h) {
+  const uint32_t sign = (uint32_t)(h & 0x8000u) << 16;
+  const uint32_t e = (h >> 10) & 0x1fu;
+  const uint32_t m = h & 0x3ffu;
+  uint32_t x;
+  if (e == 0) {
+    if (m == 0) {
+      x = sign;
+    } else { // subnormal: m * 2^-24, exact in binary32
+      float v = (float)m * 5.9604644775390625e-8f;
+      std::memcpy(&x, &v, 4);
+      x |= sign;
+    }
+  } else if (e == 31) {
+    x = sign | 0x7f800000u | (m << 13);
+  } else {
+    x = sign | ((e + 112u) << 23) | (m << 13);
+  }
+  float f;
+  std::memcpy(&f, &x, 4);
+  return f;
+}
+
+int bits_of(int fmt) { return fmt == KVFO_F16 ? 16 : fmt == KVFO_INT8 ? 8 : 4; }
+
+} // namespace
+
+extern "C" {
+
+uint16_t kvfo_f2h(float f) { return f2h(f); }
+float kvfo_h2f(uint16_t h) { return h2f(h); }
+
+void kvfo_f2h_array(const float *x, uint16_t *out, long long n) {
+  for (long long i = 0; i < n; ++i) out[i] = f2h(x[i]);
+}
+
+void kvfo_h2f_array(const uint16_t *x, float *out, long long n) {
+  for (long long i = 0; i < n; ++i) out[i] = h2f(x[i]);
+}
+
+uint64_t kvfo_mt64_10000th(void) {
+  std::mt19937_64 g; // default seed 5489
+  g.discard(9999);
+  return g();
+}
+
+void kvfo_mt64_raw(uint64_t seed, uint64_t *out, long long count) {
+  std::mt19937_64 g(seed);
+  for (long long i = 0; i < count; ++i) out[i] = g();
+}
+
+void kvfo_normal(uint64_t seed, float *out, long long count) {
+  std::mt19937_64 g(seed);
+  std::normal_distribution<float> nd(0.f, 1.f);
+  for (long long i = 0; i < count; ++i) out[i] = nd(g);
+}
+
+// runtime/kvf_host.h:51-61: one generator, one distribution, q then K then V.
+void kvfo_make_data(int B, int H, int Hkv, int D, int n, uint64_t seed,
+                    float *q, float *K, float *V) {
+  std::mt19937_64 g(seed);
+  std::normal_distribution<float> nd(0.f, 1.f);
+  const long long nq = (long long)B * H * D;
+  const long long nk = (long long)B * Hkv * n * D;
+  for (long long i = 0; i < nq; ++i) q[i] = nd(g);
+  for (long long i = 0; i < nk; ++i) K[i] = nd(g);
+  for (long long i = 0; i < nk; ++i) V[i] = nd(g);
+}
+
+// runtime/kvf_host.h:72-121.
+void kvfo_quantize(int fmt, int group, int D, const float *X, long long rows,
+                   uint8_t *data, uint16_t *meta, float *deq) {
+  const int rb = D * bits_of(fmt) / 8;
+  std::memset(data, 0, (size_t)rows * rb);
+  if (fmt == KVFO_F16) {
+    for (long long i = 0; i < rows * D; ++i) {
+      const uint16_t h = f2h(X[i]);
+      std::memcpy(data + 2 * i, &h, 2);
+      deq[i] = h2f(h);
+    }
+    return;
+  }
+  const int gpr = D / group;
+  const int levels = fmt == KVFO_INT8 ? 255 : 15;
+  for (long long r = 0; r < rows; ++r) {
+    for (int gi = 0; gi < gpr; ++gi) {
+      const float *x = X + r * D + (long long)gi * group;
+      float lo = x[0], hi = x[0];
+      for (int i = 1; i < group; ++i) {
+        lo = std::min(lo, x[i]);
+        hi = std::max(hi, x[i]);
+      }
+      const uint16_t zero_h = f2h(lo);
+      float scale = (hi - lo) / (float)levels;
+      if (scale <= 0.f) scale = 1.f;
+      const uint16_t scale_h = f2h(scale);
+      const float zero = h2f(zero_h);
+      const float sc = h2f(scale_h);
+      meta[2 * (r * gpr + gi)] = scale_h;
+      meta[2 * (r * gpr + gi) + 1] = zero_h;
+      for (int i = 0; i < group; ++i) {
+        const int col = gi * group + i;
+        long v = std::lround((x[i] - zero) / sc);
+        int qv = (int)std::min<long>(std::max<long>(v, 0), levels);
+        deq[r * D + col] = (float)qv * sc + zero;
+        if (fmt == KVFO_INT8) {
+          data[r * rb + col] = (uint8_t)qv;
+        } else {
+          uint8_t &byte = data[r * rb + col / 2];
+          byte = (col & 1) ? (uint8_t)((byte & 0x0F) | (qv << 4))
+                           : (uint8_t)((byte & 0xF0) | qv);
+        }
+      }
+    }
+  }
+}
+
+// runtime/kvf_host.h:156-165.
+void kvfo_page_table(long long pages, uint64_t seed, int32_t *perm) {
+  std::vector<int> p((size_t)pages);
+  std::iota(p.begin(), p.end(), 0);
+  std::mt19937_64 g(seed);
+  std::shuffle(p.begin(), p.end(), g);
+  std::copy(p.begin(), p.end(), perm);
+}
+
+// runtime/kvf_host.h:124-135.
+long long kvfo_row_of(int order, int bt, const int32_t *table, int max_blocks,
+                      int n, int Hkv, int b, int h, int t) {
+  if (bt == 0)
+    return order == KVFO_HEAD ? ((long long)b * Hkv + h) * n + t
+                              : ((long long)b * n + t) * Hkv + h;
+  const int blk = t / bt, tl = t % bt;
+  const long long page = table[(long long)b * max_blocks + blk];
+  const long long base = page * Hkv * bt;
+  return order == KVFO_HEAD ? base + (long long)h * bt + tl
+                            : base + (long long)tl * Hkv + h;
+}
+
+// runtime/kvf_host.h:166-184: logical row (b,h,t) -> physical row.
+void kvfo_place(int B, int Hkv, int n, int row_bytes, int meta_words,
+                int order, int bt, const int32_t *table, int max_blocks,
+                const uint8_t *data, const uint32_t *meta, uint8_t *pdata,
+                uint32_t *pmeta) {
+  for (int b = 0; b < B; ++b)
+    for (int h = 0; h < Hkv; ++h)
+      for (int t = 0; t < n; ++t) {
+        const long long lr = ((long long)b * Hkv + h) * n + t;
+        const long long pr = kvfo_row_of(order, bt, table, max_blocks, n, Hkv, b, h, t);
+        std::memcpy(pdata + pr * row_bytes, data + lr * row_bytes, (size_t)row_bytes);
+        if (meta_words)
+          std::memcpy(pmeta + pr * meta_words, meta + lr * meta_words,
+                      (size_t)meta_words * 4);
+      }
+}
+
+static void attend_one(int D, int n, const float *qh, const float *Kh,
+                       const float *Vh, float scale, float *out,
+                       std::vector<double> &sc, std::vector<double> &acc) {
+  double mx = -1e300;
+  for (int t = 0; t < n; ++t) {
+    const float *k = Kh + (long long)t * D;
+    double d = 0;
+    for (int c = 0; c < D; ++c) d += (double)qh[c] * k[c];
+    sc[t] = d * scale;
+    mx = std::max(mx, sc[t]);
+  }
+  double sum = 0;
+  std::fill(acc.begin(), acc.end(), 0.0);
+  for (int t = 0; t < n; ++t) {
+    const double p = std::exp(sc[t] - mx);
+    sum += p;
+    const float *v = Vh + (long long)t * D;
+    for (int c = 0; c < D; ++c) acc[c] += p * v[c];
+  }
+  for (int c = 0; c < D; ++c) out[c] = (float)(acc[c] / sum);
+}
+
+// runtime/kvf_host.h:202-234.
+void kvfo_reference_attention(int B, int H, int Hkv, int D, int n,
+                              const float *q, const float *K, const float *V,
+                              float scale, float *out) {
+  const int gq = H / Hkv;
+  std::vector<double> sc(n), acc(D);
+  for (int b = 0; b < B; ++b)
+    for (int h = 0; h < H; ++h) {
+      const int hk = h / gq;
+      const long long base = ((long long)b * Hkv + hk) * n * D;
+      attend_one(D, n, q + ((long long)b * H + h) * D, K + base, V + base, scale,
+                 out + ((long long)b * H + h) * D, sc, acc);
+    }
+}
+
+void kvfo_reference_attention_varlen(int B, int H, int Hkv, int D, int n_max,
+                                     const int32_t *lens, const float *q,
+                                     const float *K, const float *V,
+                                     float scale, float *out) {
+  const int gq = H / Hkv;
+  std::vector<double> sc(n_max > 0 ? n_max : 1), acc(D);
+  for (int b = 0; b < B; ++b)
+    for (int h = 0; h < H; ++h) {
+      const int hk = h / gq;
+      const long long base = ((long long)b * Hkv + hk) * n_max * D;
+      float *o = out + ((long long)b * H + h) * D;
+      if (lens[b] <= 0) {
+        std::fill(o, o + D, 0.f);
+        continue;
+      }
+      attend_one(D, lens[b], q + ((long long)b * H + h) * D, K + base, V + base,
+                 scale, o, sc, acc);
+    }
+}
+
+// runtime/kvf_host.h:236-244.
+double kvfo_rel_l2(const float *a, const float *ref, long long n) {
+  double num = 0, den = 0;
+  for (long long i = 0; i < n; ++i) {
+    const double d = (double)a[i] - ref[i];
+    num += d * d;
+    den += (double)ref[i] * ref[i];
+  }
+  return den > 0 ? std::sqrt(num / den) : 0;
+}
+
+// runtime/kvf_host.h:292.
+float kvfo_scale_log2(int D) {
+  return (1.0f / std::sqrt((float)D)) * 1.4426950408889634f;
+}
+
+// runtime/kvf_kernels.cuh:147-153 (chunking) and :276-281 (what a split
+// reports), evaluated exactly in double.
+void kvfo_reference_partials(int B, int H, int Hkv, int D, int n, int S,
+                             const float *q, const float *K, const float *V,
+                             float scale_log2, float *o_norm, double *lse2,
+                             double *m2) {
+  const int gq = H / Hkv;
+  const int chunk = (n + S - 1) / S;
+  std::vector<double> sc(n), acc(D);
+  for (int b = 0; b < B; ++b)
+    for (int h = 0; h < H; ++h) {
+      const int hk = h / gq;
+      const float *qh = q + ((long long)b * H + h) * D;
+      const float *Kh = K + ((long long)b * Hkv + hk) * n * D;
+      const float *Vh = V + ((long long)b * Hkv + hk) * n * D;
+      for (int s = 0; s < S; ++s) {
+        const long long head = (long long)b * H + h;
+        float *o = o_norm + (head * S + s) * D;
+        const int t0 = s * chunk, t1 = std::min(n, t0 + chunk);
+        if (t1 <= t0) {
+          std::fill(o, o + D, 0.f);
+          lse2[head * S + s] = -std::numeric_limits<double>::infinity();
+          m2[head * S + s] = -std::numeric_limits<double>::infinity();
+          continue;
+        }
+        double mx = -std::numeric_limits<double>::infinity();
+        for (int t = t0; t < t1; ++t) {
+          double d = 0;
+          for (int c = 0; c < D; ++c) d += (double)qh[c] * Kh[(long long)t * D + c];
+          sc[t] = d * (double)scale_log2;
+          mx = std::max(mx, sc[t]);
+        }
+        double sum = 0;
+        std::fill(acc.begin(), acc.end(), 0.0);
+        for (int t = t0; t < t1; ++t) {
+          const double p = std::exp2(sc[t] - mx);
+          sum += p;
+          for (int c = 0; c < D; ++c) acc[c] += p * Vh[(long long)t * D + c];
+        }
+        for (int c = 0; c < D; ++c) o[c] = (float)(acc[c] / sum);
+        lse2[head * S + s] = mx + std::log2(sum);
+        m2[head * S + s] = mx;
+      }
+    }
+}
+
+// runtime/kvf_kernels.cuh:288-306, in double.
+void kvfo_merge_partials(int B, int H, int D, int S, const float *part_o,
+                         const float *part_ml, float *out) {
+  for (long long head = 0; head < (long long)B * H; ++head) {
+    double M = -std::numeric_limits<double>::infinity();
+    for (int s = 0; s < S; ++s) M = std::max(M, (double)part_ml[(head * S + s) * 2]);
+    for (int c = 0; c < D; ++c) {
+      double L = 0, O = 0;
+      for (int s = 0; s < S; ++s) {
+        const double ms = part_ml[(head * S + s) * 2];
+        if (ms == -std::numeric_limits<double>::infinity()) continue;
+        const double w = std::exp2(ms - M);
+        L += part_ml[(head * S + s) * 2 + 1] * w;
+        O += part_o[(head * S + s) * D + c] * w;
+      }
+      out[head * D + c] = L > 0 ? (float)(O / L) : 0.f;
+    }
+  }
+}
+
+int kvfo_inject_outliers(int B, int Hkv, int D, int n, uint64_t seed,
+                         double frac, float factor, float *K, float *V,
+                         int32_t *chosen) {
+  const int total = Hkv * D;
+  const int k = (int)std::ceil(frac * total - 1e-9);
+  std::vector<int> p(total);
+  std::iota(p.begin(), p.end(), 0);
+  std::mt19937_64 g(seed);
+  std::shuffle(p.begin(), p.end(), g);
+  for (int i = 0; i < k; ++i) {
+    const int h = p[i] / D, c = p[i] % D;
+    if (chosen) chosen[i] = p[i];
+    for (int b = 0; b < B; ++b)
+      for (int t = 0; t < n; ++t) {
+        const long long idx = (((long long)b * Hkv + h) * n + t) * D + c;
+        K[idx] *= factor;
+        V[idx] *= factor;
+      }
+  }
+  return k;
+}
+
+void kvfo_varlen_lengths(int B, int lo, int hi, uint64_t seed, int32_t *lens) {
+  std::mt19937_64 g(seed);
+  std::uniform_int_distribution<int> u(0, hi - lo);
+  for (int b = 0; b < B; ++b) lens[b] = lo + u(g);
+}
+
+int kvfo_pool_table(int B, const int32_t *lens, int bt, int pool,
+                    uint64_t seed, int max_blocks, int32_t *table) {
+  std::vector<int> p(pool);
+  std::iota(p.begin(), p.end(), 0);
+  std::mt19937_64 g(seed);
+  std::shuffle(p.begin(), p.end(), g);
+  int next = 0;
+  for (int b = 0; b < B; ++b) {
+    const int need = (lens[b] + bt - 1) / bt;
+    for (int i = 0; i < max_blocks; ++i) {
+      if (i < need) {
+        if (next >= pool) return -1;
+        table[(long long)b * max_blocks + i] = p[next++];
+      } else {
+        table[(long long)b * max_blocks + i] = -1;
+      }
+    }
+  }
+  return next;
+}
+
+} // extern "C"

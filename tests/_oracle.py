@@ -1,0 +1,243 @@
+"""ctypes bindings for the CPU oracle (oracle/liboracle.so).
+
+Test infrastructure: only tests/, __graft_entry__.smoke() and bench.py's
+cpu_baseline leg load this. The library is built by __graft_entry__.build();
+if it is missing it is built here once (g++ only, no GPU needed).
+"""
+import ctypes
+import math
+import os
+import subprocess
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+ORACLE_DIR = os.path.join(ROOT, "oracle")
+LIB_PATH = os.path.join(ORACLE_DIR, "liboracle.so")
+REF_KVF = os.path.join(ORACLE_DIR, "_ref", "kvf_ref")
+
+F16, INT8, INT4 = 0, 1, 2
+HEAD, TOKEN = 0, 1
+
+_lib = None
+
+_p = ctypes.c_void_p
+_i = ctypes.c_int
+_ll = ctypes.c_longlong
+_u64 = ctypes.c_uint64
+_f = ctypes.c_float
+_d = ctypes.c_double
+
+
+def _ptr(a):
+    return a.ctypes.data_as(ctypes.c_void_p) if a is not None else None
+
+
+def lib():
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not os.path.exists(LIB_PATH):
+        subprocess.run(["make", "-C", ORACLE_DIR, "liboracle.so"], check=True,
+                       stdout=subprocess.DEVNULL)
+    L = ctypes.CDLL(LIB_PATH)
+    sig = {
+        "kvfo_f2h": (ctypes.c_uint16, [_f]),
+        "kvfo_h2f": (_f, [ctypes.c_uint16]),
+        "kvfo_f2h_array": (None, [_p, _p, _ll]),
+        "kvfo_h2f_array": (None, [_p, _p, _ll]),
+        "kvfo_mt64_10000th": (_u64, []),
+        "kvfo_mt64_raw": (None, [_u64, _p, _ll]),
+        "kvfo_normal": (None, [_u64, _p, _ll]),
+        "kvfo_make_data": (None, [_i, _i, _i, _i, _i, _u64, _p, _p, _p]),
+        "kvfo_quantize": (None, [_i, _i, _i, _p, _ll, _p, _p, _p]),
+        "kvfo_page_table": (None, [_ll, _u64, _p]),
+        "kvfo_row_of": (_ll, [_i, _i, _p, _i, _i, _i, _i, _i, _i]),
+        "kvfo_place": (None, [_i, _i, _i, _i, _i, _i, _i, _p, _i, _p, _p, _p, _p]),
+        "kvfo_reference_attention": (None, [_i, _i, _i, _i, _i, _p, _p, _p, _f, _p]),
+        "kvfo_reference_attention_varlen": (None, [_i, _i, _i, _i, _i, _p, _p, _p, _p, _f, _p]),
+        "kvfo_rel_l2": (_d, [_p, _p, _ll]),
+        "kvfo_scale_log2": (_f, [_i]),
+        "kvfo_reference_partials": (None, [_i, _i, _i, _i, _i, _i, _p, _p, _p, _f, _p, _p, _p]),
+        "kvfo_merge_partials": (None, [_i, _i, _i, _i, _p, _p, _p]),
+        "kvfo_inject_outliers": (_i, [_i, _i, _i, _i, _u64, _d, _f, _p, _p, _p]),
+        "kvfo_varlen_lengths": (None, [_i, _i, _i, _u64, _p]),
+        "kvfo_pool_table": (_i, [_i, _p, _i, _i, _u64, _i, _p]),
+    }
+    for name, (res, args) in sig.items():
+        fn = getattr(L, name)
+        fn.restype = res
+        fn.argtypes = args
+    _lib = L
+    return L
+
+
+def bits(fmt):
+    return {F16: 16, INT8: 8, INT4: 4}[fmt]
+
+
+def row_bytes(fmt, D):
+    return D * bits(fmt) // 8
+
+
+def f2h(x):
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    out = np.empty(x.shape, dtype=np.uint16)
+    lib().kvfo_f2h_array(_ptr(x), _ptr(out), x.size)
+    return out
+
+
+def h2f(h):
+    h = np.ascontiguousarray(h, dtype=np.uint16)
+    out = np.empty(h.shape, dtype=np.float32)
+    lib().kvfo_h2f_array(_ptr(h), _ptr(out), h.size)
+    return out
+
+
+def normal(seed, count):
+    out = np.empty(count, dtype=np.float32)
+    lib().kvfo_normal(seed, _ptr(out), count)
+    return out
+
+
+def mt64_raw(seed, count):
+    out = np.empty(count, dtype=np.uint64)
+    lib().kvfo_mt64_raw(seed, _ptr(out), count)
+    return out
+
+
+def make_data(B, H, Hkv, D, n, seed=1):
+    q = np.empty((B, H, D), dtype=np.float32)
+    K = np.empty((B, Hkv, n, D), dtype=np.float32)
+    V = np.empty((B, Hkv, n, D), dtype=np.float32)
+    lib().kvfo_make_data(B, H, Hkv, D, n, seed, _ptr(q), _ptr(K), _ptr(V))
+    return q, K, V
+
+
+def quantize(fmt, group, D, X):
+    """Returns (data uint8 [rows, row_bytes], meta uint16 [rows, D/group, 2] or None,
+    deq float32 same shape as X)."""
+    X = np.ascontiguousarray(X, dtype=np.float32)
+    rows = X.size // D
+    data = np.empty((rows, row_bytes(fmt, D)), dtype=np.uint8)
+    meta = None
+    if fmt != F16:
+        meta = np.empty((rows, D // group, 2), dtype=np.uint16)
+    deq = np.empty(X.shape, dtype=np.float32)
+    lib().kvfo_quantize(fmt, group, D, _ptr(X), rows, _ptr(data), _ptr(meta), _ptr(deq))
+    return data, meta, deq
+
+
+def page_table(pages, seed):
+    out = np.empty(pages, dtype=np.int32)
+    lib().kvfo_page_table(pages, seed, _ptr(out))
+    return out
+
+
+def row_of(order, bt, table, max_blocks, n, Hkv, b, h, t):
+    return lib().kvfo_row_of(order, bt, _ptr(table), max_blocks, n, Hkv, b, h, t)
+
+
+def place(B, Hkv, n, fmt, group, D, order, bt, data, meta, seed=18, table=None):
+    """Host placement as upload_cache does it: returns (pdata, pmeta, table, max_blocks)."""
+    rb = row_bytes(fmt, D)
+    mw = 0 if fmt == F16 else D // group
+    max_blocks = 0
+    if bt:
+        max_blocks = (n + bt - 1) // bt
+        if table is None:
+            table = page_table(B * max_blocks, seed)
+        rows_alloc = B * max_blocks * Hkv * bt
+    else:
+        table = None
+        rows_alloc = B * Hkv * n
+    pdata = np.zeros((rows_alloc, rb), dtype=np.uint8)
+    pmeta = np.zeros((rows_alloc, max(mw, 1)), dtype=np.uint32) if mw else None
+    meta32 = None if meta is None else np.ascontiguousarray(meta).view(np.uint32).reshape(-1, mw)
+    lib().kvfo_place(B, Hkv, n, rb, mw, order, bt,
+                     _ptr(table) if table is not None else None, max_blocks,
+                     _ptr(np.ascontiguousarray(data)), _ptr(meta32), _ptr(pdata), _ptr(pmeta))
+    return pdata, pmeta, table, max_blocks
+
+
+def reference_attention(q, K, V, scale=None):
+    B, H, D = q.shape
+    _, Hkv, n, _ = K.shape
+    if scale is None:
+        scale = 1.0 / math.sqrt(D)
+        scale = float(np.float32(1.0) / np.sqrt(np.float32(D)))
+    out = np.empty((B, H, D), dtype=np.float32)
+    lib().kvfo_reference_attention(B, H, Hkv, D, n, _ptr(np.ascontiguousarray(q)),
+                                   _ptr(np.ascontiguousarray(K)),
+                                   _ptr(np.ascontiguousarray(V)), scale, _ptr(out))
+    return out
+
+
+def reference_attention_varlen(q, K, V, lens, scale=None):
+    B, H, D = q.shape
+    _, Hkv, n_max, _ = K.shape
+    if scale is None:
+        scale = float(np.float32(1.0) / np.sqrt(np.float32(D)))
+    lens = np.ascontiguousarray(lens, dtype=np.int32)
+    out = np.empty((B, H, D), dtype=np.float32)
+    lib().kvfo_reference_attention_varlen(B, H, Hkv, D, n_max, _ptr(lens),
+                                          _ptr(np.ascontiguousarray(q)),
+                                          _ptr(np.ascontiguousarray(K)),
+                                          _ptr(np.ascontiguousarray(V)), scale, _ptr(out))
+    return out
+
+
+def rel_l2(a, ref):
+    a = np.ascontiguousarray(a, dtype=np.float32)
+    ref = np.ascontiguousarray(ref, dtype=np.float32)
+    return lib().kvfo_rel_l2(_ptr(a), _ptr(ref), a.size)
+
+
+def scale_log2(D):
+    return lib().kvfo_scale_log2(D)
+
+
+def reference_partials(q, K, V, S):
+    B, H, D = q.shape
+    _, Hkv, n, _ = K.shape
+    o = np.empty((B, H, S, D), dtype=np.float32)
+    lse = np.empty((B, H, S), dtype=np.float64)
+    m2 = np.empty((B, H, S), dtype=np.float64)
+    lib().kvfo_reference_partials(B, H, Hkv, D, n, S, _ptr(np.ascontiguousarray(q)),
+                                  _ptr(np.ascontiguousarray(K)),
+                                  _ptr(np.ascontiguousarray(V)), scale_log2(D),
+                                  _ptr(o), _ptr(lse), _ptr(m2))
+    return o, lse, m2
+
+
+def merge_partials(part_o, part_ml):
+    B, H, S, D = part_o.shape
+    out = np.empty((B, H, D), dtype=np.float32)
+    lib().kvfo_merge_partials(B, H, D, S, _ptr(np.ascontiguousarray(part_o)),
+                              _ptr(np.ascontiguousarray(part_ml)), _ptr(out))
+    return out
+
+
+def inject_outliers(K, V, seed=1001, frac=0.01, factor=8.0):
+    B, Hkv, n, D = K.shape
+    chosen = np.empty(Hkv * D, dtype=np.int32)
+    k = lib().kvfo_inject_outliers(B, Hkv, D, n, seed, frac, factor, _ptr(K), _ptr(V),
+                                   _ptr(chosen))
+    return chosen[:k].copy()
+
+
+def varlen_lengths(B, lo, hi, seed):
+    out = np.empty(B, dtype=np.int32)
+    lib().kvfo_varlen_lengths(B, lo, hi, seed, _ptr(out))
+    return out
+
+
+def pool_table(lens, bt, pool, seed):
+    lens = np.ascontiguousarray(lens, dtype=np.int32)
+    B = lens.size
+    max_blocks = int((int(lens.max()) + bt - 1) // bt)
+    table = np.empty((B, max_blocks), dtype=np.int32)
+    used = lib().kvfo_pool_table(B, _ptr(lens), bt, pool, seed, max_blocks, _ptr(table))
+    if used < 0:
+        raise ValueError("pool too small")
+    return table, max_blocks
