@@ -1,0 +1,141 @@
+/* kvf_abi.h - the drop-in boundary of KVForge's decode-attention path, MI355X.
+ *
+ * This header replaces the ABI part of the reference's
+ * runtime/kvf_kernels.cuh (Args, Fmt, Ord: lines 26-46) and the extern "C"
+ * launcher that src/codegen.cpp:79-91 emits. A plan compiled for the
+ * reference drops in unchanged: the same Args layout (9 pointers, 9 ints, one
+ * float, in the same order), the same variant ids, the same plan-override
+ * semantics (a launcher overwrites splits, warps, group_shift, block_shift),
+ * the same error behaviour (the launch error is returned, faults surface at
+ * the caller's next synchronisation, nothing is allocated and no host sync is
+ * made), with hipError_t / hipStream_t in place of the CUDA types.
+ *
+ * MI355X meaning of the scheduling fields: `warps` is the number of 64-lane
+ * wavefronts per workgroup (4 or 8), not 32-thread warps.
+ */
+#ifndef KVF_ABI_H
+#define KVF_ABI_H
+
+#include <stdint.h>
+#include <hip/hip_runtime_api.h>
+
+#ifdef __cplusplus
+#include <hip/hip_fp16.h>
+namespace kvf {
+
+/* runtime/kvf_kernels.cuh:26-27 */
+enum Fmt { FMT_F16 = 0, FMT_INT8 = 1, FMT_INT4 = 2 };
+enum Ord { ORD_HEAD = 0, ORD_TOKEN = 1 };
+
+/* runtime/kvf_kernels.cuh:29-46, field for field. */
+struct Args {
+  const float *q;          /* [B][H][D], fp32 */
+  const unsigned char *k;  /* K payload, rows of D*bits/8 bytes */
+  const unsigned char *v;  /* V payload */
+  const __half2 *k_meta;   /* [rows][D/group] (scale, zero), quantized only */
+  const __half2 *v_meta;
+  const int *block_table;  /* [B][max_blocks] page ids, paged layouts only */
+  float *out;              /* [B][H][D], fp32 */
+  float *part_o;           /* [B][H][splits][D] unnormalised partial output */
+  float *part_ml;          /* [B][H][splits][2] running max (log2) and sum */
+  int B, H, Hkv, n;
+  int splits;              /* chunks of the KV length per head */
+  int warps;               /* 64-lane wavefronts per workgroup (4 or 8) */
+  int group_shift;         /* log2(quantization group), quantized only */
+  int block_shift;         /* log2(tokens per page), paged only */
+  int max_blocks;          /* pages per sequence in the block table */
+  float scale_log2;        /* softmax scale * log2(e) */
+};
+
+/* Additive extension for variable-length batches out of a shared block pool
+ * with optional f16 query/output (no counterpart in the reference's Args,
+ * which has one n for every sequence and fp32 q/out only,
+ * runtime/kvf_kernels.cuh:30-39). Args stays byte-identical; these fields
+ * travel beside it. */
+struct VarlenArgs {
+  const int *seq_lens;     /* [B] tokens per sequence; Args::n is the maximum */
+  const void *q16;         /* [B][H][D] binary16 query, or NULL to use Args::q */
+  void *out16;             /* [B][H][D] binary16 output, or NULL to use Args::out */
+};
+
+} /* namespace kvf */
+typedef kvf::Args kvf_args_t;
+typedef kvf::VarlenArgs kvf_varlen_args_t;
+#else
+/* The same layout for C callers. */
+typedef struct kvf_args {
+  const float *q;
+  const unsigned char *k, *v;
+  const void *k_meta, *v_meta;
+  const int *block_table;
+  float *out, *part_o, *part_ml;
+  int B, H, Hkv, n, splits, warps, group_shift, block_shift, max_blocks;
+  float scale_log2;
+} kvf_args_t;
+typedef struct kvf_varlen_args {
+  const int *seq_lens;
+  const void *q16;
+  void *out16;
+} kvf_varlen_args_t;
+#endif
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---- dispatch by variant id ------------------------------------------------
+ * Variant ids are the reference's: "{fmt}_{hm|tm}_{c|p}_g{G}_u{U}_d{D}"
+ * (src/codegen.cpp:59-65), e.g. "int8_hm_c_g4_u2_d128". These entry points
+ * are the C-ABI face of kvf::Registry (runtime/kvf_registry.h:15-24) for
+ * callers outside C++ (ctypes, cgo); the registry lookup plus
+ * `fn(a, st)` is exactly what bench/sweep.cu:180-186 does. */
+
+/* Launch one decode step (partial kernel, plus the merge when a->splits > 1)
+ * with the caller's Args unchanged. Returns hipErrorNotFound for an unknown
+ * id, hipErrorInvalidValue for arguments the kernels cannot run (for
+ * example warps outside {4, 8} or a group the format does not offer),
+ * otherwise the launch status. */
+hipError_t kvf_launch_variant(const char *variant_id, const kvf_args_t *a,
+                              hipStream_t stream);
+
+/* As kvf_launch_variant, for the variable-length / block-pool extension. */
+hipError_t kvf_launch_varlen_variant(const char *variant_id, const kvf_args_t *a,
+                                     const kvf_varlen_args_t *va,
+                                     hipStream_t stream);
+
+/* Only the partial (split) kernel of a variant, writing part_o / part_ml
+ * even when splits == 1; for measuring the streaming kernel by itself. */
+hipError_t kvf_launch_partial_variant(const char *variant_id, const kvf_args_t *a,
+                                      hipStream_t stream);
+
+/* Only the log-sum-exp merge (runtime/kvf_kernels.cuh:288-306) of the
+ * partials named by `a` (B, H, splits, part_o, part_ml, out) for head
+ * dimension d. */
+hipError_t kvf_launch_merge(int d, const kvf_args_t *a, hipStream_t stream);
+
+/* Number of registered variants and the id of the i-th one. */
+int kvf_variant_count(void);
+const char *kvf_variant_id(int i);
+
+/* ---- KV append / quantize (the step before the path) ----------------------
+ * Quantize `rows` logical rows of `d` fp32 values (device memory, row r is
+ * sequence b = r / (Hkv*n), head h = (r / n) % Hkv, token t = r % n) in the
+ * format (fmt, group) and write each row to its physical row of the
+ * (order, paged) layout: codes into `data`, (scale, zero) binary16 pairs
+ * into `meta` (NULL for f16). Bit-exact with the reference's host quantizer
+ * (runtime/kvf_host.h:72-121) and placement (runtime/kvf_host.h:124-135,
+ * 166-184). `block_table` is [B][max_blocks] when block_tokens > 0. */
+hipError_t kvf_quantize_place(int fmt, int group, int d, const float *x,
+                              int B, int Hkv, int n, int order,
+                              int block_tokens, const int *block_table,
+                              int max_blocks, unsigned char *data, void *meta,
+                              hipStream_t stream);
+
+/* Library version string. */
+const char *kvf_version(void);
+
+#ifdef __cplusplus
+} /* extern "C" */
+#endif
+
+#endif /* KVF_ABI_H */

@@ -1,0 +1,280 @@
+// kvf_runtime.hip - C-ABI entry points of libkvf_hip.so.
+//
+//   kvf_launch_variant / kvf_launch_varlen_variant / kvf_launch_partial_variant
+//       dispatch a decode step by the reference's variant id
+//       (src/codegen.cpp:59-65), the way bench/sweep.cu:180-186 does through
+//       kvf::Registry;
+//   kvf_launch_merge
+//       the log-sum-exp merge alone;
+//   kvf_quantize_place
+//       the KV append step: quantize fp32 rows on the GPU and scatter them to
+//       their physical rows, bit-exact with runtime/kvf_host.h:72-135,166-184.
+#include "kvf_kernels.hpp"
+
+#include <algorithm>
+#include <cstdio>
+#include <cstdlib>
+#include <cstring>
+#include <mutex>
+#include <string>
+#include <vector>
+
+namespace kvf {
+namespace gfx950 {
+namespace {
+
+struct Variant {
+  int fmt = -1, ord = -1, paged = -1, g = 0, u = 0, d = 0;
+};
+
+// "{fmt}_{hm|tm}_{c|p}_g{G}_u{U}_d{D}"
+bool parse_variant(const char *id, Variant &v) {
+  if (!id) return false;
+  char fmt[8] = {0}, ord[4] = {0}, res[4] = {0};
+  int g = 0, u = 0, d = 0, used = 0;
+  if (std::sscanf(id, "%7[a-z0-9]_%2[a-z]_%1[a-z]_g%d_u%d_d%d%n", fmt, ord, res, &g, &u, &d,
+                  &used) != 6 || id[used] != '\0')
+    return false;
+  const std::string f(fmt), o(ord), r(res);
+  v.fmt = f == "f16" ? FMT_F16 : f == "int8" ? FMT_INT8 : f == "int4" ? FMT_INT4 : -1;
+  v.ord = o == "hm" ? ORD_HEAD : o == "tm" ? ORD_TOKEN : -1;
+  v.paged = r == "c" ? 0 : r == "p" ? 1 : -1;
+  v.g = g; v.u = u; v.d = d;
+  return v.fmt >= 0 && v.ord >= 0 && v.paged >= 0 && (g == 1 || g == 2 || g == 4 || g == 8) &&
+         (u == 2 || u == 4) && (d == 64 || d == 128);
+}
+
+struct Call {
+  const Args &a;
+  const Ext &x;
+  bool partial;
+  hipStream_t st;
+};
+
+template <int FMT, int D, int G, int U, int ORD, bool PAGED>
+hipError_t go(const Call &c) {
+  return launch_ext<FMT, D, G, U, ORD, PAGED>(c.a, c.x, c.partial, c.st);
+}
+
+template <int FMT, int D, int G, int U>
+hipError_t by_layout(const Variant &v, const Call &c) {
+  if (v.ord == ORD_HEAD)
+    return v.paged ? go<FMT, D, G, U, ORD_HEAD, true>(c) : go<FMT, D, G, U, ORD_HEAD, false>(c);
+  return v.paged ? go<FMT, D, G, U, ORD_TOKEN, true>(c) : go<FMT, D, G, U, ORD_TOKEN, false>(c);
+}
+
+template <int FMT, int D, int G>
+hipError_t by_unroll(const Variant &v, const Call &c) {
+  return v.u == 2 ? by_layout<FMT, D, G, 2>(v, c) : by_layout<FMT, D, G, 4>(v, c);
+}
+
+template <int FMT, int D>
+hipError_t by_pack(const Variant &v, const Call &c) {
+  switch (v.g) {
+  case 1: return by_unroll<FMT, D, 1>(v, c);
+  case 2: return by_unroll<FMT, D, 2>(v, c);
+  case 4: return by_unroll<FMT, D, 4>(v, c);
+  default: return by_unroll<FMT, D, 8>(v, c);
+  }
+}
+
+template <int FMT>
+hipError_t by_dim(const Variant &v, const Call &c) {
+  return v.d == 128 ? by_pack<FMT, 128>(v, c) : by_pack<FMT, 64>(v, c);
+}
+
+hipError_t dispatch(const Variant &v, const Call &c) {
+  switch (v.fmt) {
+  case FMT_F16: return by_dim<FMT_F16>(v, c);
+  case FMT_INT8: return by_dim<FMT_INT8>(v, c);
+  default: return by_dim<FMT_INT4>(v, c);
+  }
+}
+
+Registry &registry() {
+  static Registry reg;
+  static std::once_flag once;
+  std::call_once(once, [] { kvf_register_all(reg); });
+  return reg;
+}
+
+std::vector<std::string> &variant_ids() {
+  static std::vector<std::string> ids;
+  static std::once_flag once;
+  std::call_once(once, [] {
+    for (const auto &kv : registry().fn) ids.push_back(kv.first);
+    std::sort(ids.begin(), ids.end());
+  });
+  return ids;
+}
+
+// ---------------------------------------------------------------- quantizer
+template <int FMT>
+__global__ void __launch_bounds__(256)
+quantize_place_kernel(const float *__restrict__ x, long long rows, int d, int group, int Hkv,
+                      int n, int order, int bt, const int *table, int max_blocks,
+                      unsigned char *data, uint32_t *meta) {
+  const int lane = threadIdx.x & 63;
+  const long long row = (long long)blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
+  if (row >= rows) return; // whole wavefronts leave together
+  const int t = (int)(row % n);
+  const int h = (int)((row / n) % Hkv);
+  const int b = (int)(row / ((long long)n * Hkv));
+  long long prow;
+  if (bt == 0) {
+    prow = order == ORD_HEAD ? ((long long)b * Hkv + h) * n + t : ((long long)b * n + t) * Hkv + h;
+  } else {
+    const long long page = table[(long long)b * max_blocks + t / bt];
+    const long long base = page * Hkv * bt;
+    prow = order == ORD_HEAD ? base + (long long)h * bt + t % bt
+                             : base + (long long)(t % bt) * Hkv + h;
+  }
+  const float *xr = x + row * d;
+  const int per = d / 64; // elements per lane: column = e*64 + lane
+  if constexpr (FMT == FMT_F16) {
+    for (int e = 0; e < per; ++e) {
+      const int col = e * 64 + lane;
+      const _Float16 hv = (_Float16)xr[col];
+      reinterpret_cast<_Float16 *>(data)[prow * d + col] = hv;
+    }
+    return;
+  } else {
+    const int levels = FMT == FMT_INT8 ? 255 : 15;
+    const int rb = FMT == FMT_INT8 ? d : d / 2;
+    const int gpr = d / group;
+    float xv[2];
+    for (int e = 0; e < per; ++e) xv[e] = xr[e * 64 + lane];
+    // min/max over each group: groups of 32 are lane halves, 64 one slot,
+    // 128 both slots of a 64-wide row pair
+    const int span = group < 64 ? group : 64;
+    float lo[2], hi[2];
+    for (int e = 0; e < per; ++e) {
+      lo[e] = xv[e];
+      hi[e] = xv[e];
+      for (int m = 1; m < span; m <<= 1) {
+        lo[e] = fminf(lo[e], __shfl_xor(lo[e], m));
+        hi[e] = fmaxf(hi[e], __shfl_xor(hi[e], m));
+      }
+    }
+    if (group == 128 && per == 2) {
+      lo[0] = lo[1] = fminf(lo[0], lo[1]);
+      hi[0] = hi[1] = fmaxf(hi[0], hi[1]);
+    }
+    for (int e = 0; e < per; ++e) {
+      const int col = e * 64 + lane;
+      const _Float16 zero_h = (_Float16)lo[e];
+      float scale = __fdiv_rn(hi[e] - lo[e], (float)levels);
+      if (scale <= 0.f) scale = 1.f;
+      const _Float16 scale_h = (_Float16)scale;
+      const float zero = (float)zero_h;
+      const float sc = (float)scale_h;
+      const float qf = roundf(__fdiv_rn(xv[e] - zero, sc)); // half away from zero
+      const int qv = (int)fminf(fmaxf(qf, 0.f), (float)levels);
+      const int gi = col / group;
+      if (col % group == 0) {
+        const uint32_t w = (uint32_t)__builtin_bit_cast(uint16_t, scale_h) |
+                           ((uint32_t)__builtin_bit_cast(uint16_t, zero_h) << 16);
+        meta[prow * gpr + gi] = w;
+      }
+      if constexpr (FMT == FMT_INT8) {
+        data[prow * rb + col] = (unsigned char)qv;
+      } else {
+        const int hi_code = __shfl_down(qv, 1);
+        if ((col & 1) == 0)
+          data[prow * rb + col / 2] = (unsigned char)(qv | (hi_code << 4));
+      }
+    }
+  }
+}
+
+} // namespace
+} // namespace gfx950
+} // namespace kvf
+
+using namespace kvf;
+using namespace kvf::gfx950;
+
+extern "C" hipError_t kvf_launch_variant(const char *id, const kvf_args_t *a, hipStream_t st) {
+  if (!a) return hipErrorInvalidValue;
+  const LaunchFn fn = registry().find(id ? id : "");
+  if (!fn) return hipErrorNotFound;
+  return fn(*a, st);
+}
+
+extern "C" hipError_t kvf_launch_varlen_variant(const char *id, const kvf_args_t *a,
+                                                const kvf_varlen_args_t *va, hipStream_t st) {
+  Variant v;
+  if (!a || !parse_variant(id, v)) return a ? hipErrorNotFound : hipErrorInvalidValue;
+  if (!registry().find(id)) return hipErrorNotFound;
+  Ext x;
+  if (va) {
+    x.seq_lens = va->seq_lens;
+    x.q16 = static_cast<const _Float16 *>(va->q16);
+    x.out16 = static_cast<_Float16 *>(va->out16);
+  }
+  return dispatch(v, Call{*a, x, false, st});
+}
+
+extern "C" hipError_t kvf_launch_partial_variant(const char *id, const kvf_args_t *a,
+                                                 hipStream_t st) {
+  Variant v;
+  if (!a || !parse_variant(id, v)) return a ? hipErrorNotFound : hipErrorInvalidValue;
+  if (!registry().find(id)) return hipErrorNotFound;
+  if (!a->part_o || !a->part_ml) return hipErrorInvalidValue;
+  return dispatch(v, Call{*a, Ext{}, true, st});
+}
+
+extern "C" hipError_t kvf_launch_merge(int d, const kvf_args_t *a, hipStream_t st) {
+  if (!a || a->splits < 1 || a->B < 1 || a->H < 1 || !a->part_o || !a->part_ml || !a->out)
+    return hipErrorInvalidValue;
+  if (d == 128)
+    hipLaunchKernelGGL((decode_merge<128>), dim3(a->H, a->B), dim3(64), 0, st, *a, Ext{});
+  else if (d == 64)
+    hipLaunchKernelGGL((decode_merge<64>), dim3(a->H, a->B), dim3(64), 0, st, *a, Ext{});
+  else
+    return hipErrorInvalidValue;
+  return hipGetLastError();
+}
+
+extern "C" int kvf_variant_count(void) { return (int)variant_ids().size(); }
+
+extern "C" const char *kvf_variant_id(int i) {
+  const auto &ids = variant_ids();
+  return (i >= 0 && i < (int)ids.size()) ? ids[i].c_str() : nullptr;
+}
+
+extern "C" hipError_t kvf_quantize_place(int fmt, int group, int d, const float *x, int B,
+                                         int Hkv, int n, int order, int block_tokens,
+                                         const int *block_table, int max_blocks,
+                                         unsigned char *data, void *meta, hipStream_t st) {
+  if (!x || !data || B < 1 || Hkv < 1 || n < 1 || (d != 64 && d != 128)) return hipErrorInvalidValue;
+  if (order != ORD_HEAD && order != ORD_TOKEN) return hipErrorInvalidValue;
+  if (block_tokens < 0 || (block_tokens > 0 && (!block_table || max_blocks * block_tokens < n)))
+    return hipErrorInvalidValue;
+  if (fmt != FMT_F16) {
+    if (!meta || (group != 32 && group != 64 && group != 128) || group > d) return hipErrorInvalidValue;
+  }
+  const long long rows = (long long)B * Hkv * n;
+  const dim3 block(256);
+  const dim3 grid((unsigned)((rows + 3) / 4));
+  uint32_t *m = static_cast<uint32_t *>(meta);
+  switch (fmt) {
+  case FMT_F16:
+    hipLaunchKernelGGL(quantize_place_kernel<FMT_F16>, grid, block, 0, st, x, rows, d, group, Hkv,
+                       n, order, block_tokens, block_table, max_blocks, data, m);
+    break;
+  case FMT_INT8:
+    hipLaunchKernelGGL(quantize_place_kernel<FMT_INT8>, grid, block, 0, st, x, rows, d, group,
+                       Hkv, n, order, block_tokens, block_table, max_blocks, data, m);
+    break;
+  case FMT_INT4:
+    hipLaunchKernelGGL(quantize_place_kernel<FMT_INT4>, grid, block, 0, st, x, rows, d, group,
+                       Hkv, n, order, block_tokens, block_table, max_blocks, data, m);
+    break;
+  default:
+    return hipErrorInvalidValue;
+  }
+  return hipGetLastError();
+}
+
+extern "C" const char *kvf_version(void) { return "kvforge-mi355x 0.1 (gfx950)"; }

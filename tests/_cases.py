@@ -1,0 +1,115 @@
+"""Builds one decode case on the GPU from oracle-generated inputs.
+
+Inputs (q, K, V) come from the oracle's make_data (the reference's
+generator); the cache is produced on the GPU by the product's quantize/place
+kernel and checked bit-exact against the oracle's quantizer and placement.
+"""
+import dataclasses
+import math
+
+import numpy as np
+import torch
+
+import _oracle as O
+from kvforge_amd import runtime as R
+
+
+@dataclasses.dataclass
+class Case:
+    B: int
+    H: int
+    Hkv: int
+    D: int
+    n: int
+    fmt: int
+    group: int
+    order: int
+    bt: int
+    seed: int = 1
+    outliers: bool = False
+
+    def tag(self):
+        return (f"B{self.B}_H{self.H}_Hkv{self.Hkv}_D{self.D}_n{self.n}_"
+                f"{R.FMT_NAMES[self.fmt]}{self.group or ''}_"
+                f"{'hm' if self.order == 0 else 'tm'}_{'p%d' % self.bt if self.bt else 'c'}")
+
+
+class Built:
+    pass
+
+
+def build(case, check_cache=True):
+    c = case
+    q, K, V = O.make_data(c.B, c.H, c.Hkv, c.D, c.n, c.seed)
+    if c.outliers:
+        O.inject_outliers(K, V)
+    kd, km, kdeq = O.quantize(c.fmt, c.group, c.D, K)
+    vd, vm, vdeq = O.quantize(c.fmt, c.group, c.D, V)
+    pkd, pkm, table, mb = O.place(c.B, c.Hkv, c.n, c.fmt, c.group, c.D, c.order, c.bt, kd, km)
+    pvd, pvm, _, _ = O.place(c.B, c.Hkv, c.n, c.fmt, c.group, c.D, c.order, c.bt, vd, vm,
+                             table=table)
+    dev = torch.device("cuda:0")
+    b = Built()
+    b.case = c
+    b.q_host, b.kdeq, b.vdeq, b.K, b.V = q, kdeq, vdeq, K, V
+    b.q = torch.from_numpy(q).to(dev)
+    b.table = torch.from_numpy(table.astype(np.int32)).to(dev) if c.bt else None
+    b.max_blocks = mb
+    rows, _ = R.rows_alloc(c.B, c.Hkv, c.n, c.bt)
+    rb = R.row_bytes(c.fmt, c.D)
+    mw = c.D // c.group if c.fmt != R.FMT_F16 else 0
+    b.k = torch.zeros(rows * rb, dtype=torch.uint8, device=dev)
+    b.v = torch.zeros(rows * rb, dtype=torch.uint8, device=dev)
+    b.km = torch.zeros(rows * mw, dtype=torch.int32, device=dev) if mw else None
+    b.vm = torch.zeros(rows * mw, dtype=torch.int32, device=dev) if mw else None
+    Kd = torch.from_numpy(K).to(dev)
+    Vd = torch.from_numpy(V).to(dev)
+    R.quantize_place(c.fmt, c.group, c.D, Kd, c.B, c.Hkv, c.n, c.order, c.bt, b.table, mb,
+                     b.k, b.km)
+    R.quantize_place(c.fmt, c.group, c.D, Vd, c.B, c.Hkv, c.n, c.order, c.bt, b.table, mb,
+                     b.v, b.vm)
+    torch.cuda.synchronize()
+    del Kd, Vd
+    if check_cache:
+        assert np.array_equal(b.k.cpu().numpy(), pkd.ravel()), "K codes differ"
+        assert np.array_equal(b.v.cpu().numpy(), pvd.ravel()), "V codes differ"
+        if mw:
+            assert np.array_equal(b.km.cpu().numpy().view(np.uint32), pkm.ravel()), "K meta differs"
+            assert np.array_equal(b.vm.cpu().numpy().view(np.uint32), pvm.ravel()), "V meta differs"
+    b.out = torch.zeros((c.B, c.H, c.D), dtype=torch.float32, device=dev)
+    b._ref = None
+    return b
+
+
+def reference(b):
+    if b._ref is None:
+        b._ref = O.reference_attention(b.q_host, b.kdeq, b.vdeq)
+    return b._ref
+
+
+def args(b, splits, warps=4, partial_buffers=None):
+    c = b.case
+    po = pm = None
+    if splits > 1 or partial_buffers:
+        s = max(splits, 1)
+        po = torch.full((c.B, c.H, s, c.D), float("nan"), device=b.q.device)
+        pm = torch.full((c.B, c.H, s, 2), float("nan"), device=b.q.device)
+    a = R.make_args(b.q, b.k, b.v, b.km, b.vm, b.table, b.out, po, pm, c.B, c.H, c.Hkv, c.n,
+                    splits, warps, group=c.group if c.fmt != R.FMT_F16 else 0,
+                    block_tokens=c.bt, max_blocks=b.max_blocks, D=c.D)
+    a._keep = (po, pm)
+    return a
+
+
+def vid(b, pack, unroll):
+    c = b.case
+    g = c.H // c.Hkv if pack else 1
+    return R.variant_id(c.fmt, c.order, c.bt > 0, g, unroll, c.D)
+
+
+def run(b, splits, pack=True, unroll=2, warps=4):
+    b.out.fill_(float("nan"))
+    a = args(b, splits, warps)
+    R.launch(vid(b, pack, unroll), a)
+    torch.cuda.synchronize()
+    return b.out.cpu().numpy()

@@ -1,0 +1,225 @@
+"""GPU parity of the decode-attention path, through the C-ABI.
+
+Bar (the reference's own, bench/sweep.cu:194-197 and runtime/kvf_driver.cu:52):
+relative L2 error against the double-precision attention over the same
+dequantised cache below 2e-3; for f16 caches also max-abs <= 2e-3. The
+cache itself (codes, scales, paged placement) must be bit-exact.
+"""
+import math
+import sys
+
+import numpy as np
+import pytest
+import torch
+
+import _oracle as O
+from _cases import Case, build, reference, run, args, vid
+from kvforge_amd import runtime as R
+
+pytestmark = pytest.mark.gpu
+
+REL_TOL = 2e-3
+ABS_TOL_F16 = 2e-3
+
+
+@pytest.fixture(scope="module", autouse=True)
+def _gpu():
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU")
+    R.hip_lib()
+
+
+def say(*a):
+    print(*a, flush=True)
+    sys.stdout.flush()
+
+
+def check(b, got, what):
+    ref = reference(b)
+    err = O.rel_l2(got, ref)
+    mx = float(np.max(np.abs(got - ref)))
+    say(f"  {b.case.tag()} {what}: rel_l2={err:.3g} max_abs={mx:.3g}")
+    assert np.all(np.isfinite(got)), what
+    assert err < REL_TOL, (what, err)
+    if b.case.fmt == R.FMT_F16:
+        assert mx <= ABS_TOL_F16, (what, mx)
+    return err
+
+
+def test_registry_has_reference_ids():
+    ids = set(R.variants())
+    for v in ["f16_hm_c_g1_u2_d128", "int8_hm_c_g4_u2_d128", "int4_tm_p_g8_u4_d64",
+              "int8_tm_p_g4_u4_d128"]:
+        assert v in ids
+    assert len(ids) == 3 * 2 * 2 * 2 * 4 * 2
+
+
+def test_config1_mha_f16_plumbing():
+    # MHA, B1, 32 heads, d128, n4096, f16 head-major, S=1
+    b = build(Case(1, 32, 32, 128, 4096, R.FMT_F16, 0, R.ORD_HEAD, 0))
+    check(b, run(b, 1, pack=False), "S=1")
+    check(b, run(b, 8, pack=False, unroll=4, warps=8), "S=8")
+
+
+@pytest.mark.parametrize("fmt,group", [(R.FMT_F16, 0), (R.FMT_INT8, 64), (R.FMT_INT4, 32)])
+@pytest.mark.parametrize("order", [R.ORD_HEAD, R.ORD_TOKEN])
+@pytest.mark.parametrize("bt", [0, 16])
+def test_twelve_variants(fmt, group, order, bt):
+    b = build(Case(2, 32, 8, 128, 1000, fmt, group, order, bt, seed=3))
+    for pack in (True, False):
+        for splits in (1, 4):
+            check(b, run(b, splits, pack=pack, unroll=2 if splits == 1 else 4,
+                         warps=4 if pack else 8), f"pack={pack} S={splits}")
+
+
+@pytest.mark.parametrize("fmt,group", [(R.FMT_INT8, 128), (R.FMT_INT4, 64), (R.FMT_INT4, 128),
+                                       (R.FMT_INT8, 32)])
+def test_other_groups(fmt, group):
+    b = build(Case(1, 16, 4, 128, 700, fmt, group, R.ORD_HEAD, 0, seed=4))
+    check(b, run(b, 3), "S=3")
+
+
+@pytest.mark.parametrize("fmt,group", [(R.FMT_F16, 0), (R.FMT_INT8, 64), (R.FMT_INT4, 32),
+                                       (R.FMT_INT4, 64)])
+@pytest.mark.parametrize("bt", [0, 32])
+def test_d64(fmt, group, bt):
+    b = build(Case(2, 16, 2, 64, 777, fmt, group, R.ORD_TOKEN if bt else R.ORD_HEAD, bt, seed=5))
+    check(b, run(b, 2), "S=2")
+    check(b, run(b, 1, pack=False), "S=1 unpacked")
+
+
+# tests/edge/*.kv of the reference: shapes that stress chunking and packing
+EDGE = [
+    ("edge_short", 1, 8, 8, 64, 100),
+    ("edge_n129", 1, 32, 8, 128, 129),
+    ("edge_odd_n", 2, 12, 4, 128, 1001),
+    ("edge_g8_n3333", 3, 16, 2, 64, 3333),
+]
+
+
+@pytest.mark.parametrize("name,B,H,Hkv,D,n", EDGE)
+def test_edge_shapes(name, B, H, Hkv, D, n):
+    g = H // Hkv
+    for fmt, group in ((R.FMT_F16, 0), (R.FMT_INT8, 64), (R.FMT_INT4, 32)):
+        for order, bt in ((R.ORD_HEAD, 0), (R.ORD_TOKEN, 64)):
+            b = build(Case(B, H, Hkv, D, n, fmt, group, order, bt, seed=7))
+            for splits in (1, 2, 64):
+                check(b, run(b, splits, pack=g in (2, 4, 8)), f"{name} S={splits}")
+
+
+def test_empty_splits_and_partials():
+    # n < splits * 2: some splits own no token and must report (-inf, 0, 0)
+    c = Case(1, 8, 2, 128, 40, R.FMT_INT8, 64, R.ORD_HEAD, 0, seed=9)
+    b = build(c)
+    S = 32
+    a = args(b, S, 4, partial_buffers=True)
+    R.launch_partial(vid(b, True, 2), a)
+    torch.cuda.synchronize()
+    po, pm = (t.cpu().numpy() for t in a._keep)
+    o_ref, lse_ref, m_ref = O.reference_partials(b.q_host, b.kdeq, b.vdeq, S)
+    m, L = pm[..., 0].astype(np.float64), pm[..., 1].astype(np.float64)
+    empty = np.isneginf(m_ref)
+    assert np.any(empty)
+    assert np.all(np.isneginf(m[empty])) and np.all(L[empty] == 0) and np.all(po[empty] == 0)
+    full = ~empty
+    assert np.max(np.abs(m[full] - m_ref[full])) < 1e-4
+    lse = m + np.log2(np.where(L > 0, L, 1))
+    assert np.max(np.abs(lse[full] - lse_ref[full])) < 1e-4
+    # normalised partials: the reference's relative bar; V enters PV as
+    # binary16 dequantised values, so single entries of a 2-token split can
+    # differ by up to a binary16 rounding of |v| (< 2^-11 * 4 here)
+    on = po[full] / L[full][:, None]
+    assert O.rel_l2(on.astype(np.float32), o_ref[full]) < REL_TOL
+    assert np.max(np.abs(on - o_ref[full])) < 2.0 ** -11 * 4
+    # the merge of these partials equals the unsplit reference
+    out = torch.zeros_like(b.out)
+    a.out = out.data_ptr()
+    R.launch_merge(128, a)
+    torch.cuda.synchronize()
+    check(b, out.cpu().numpy(), "merge")
+
+
+def test_north_star_int8_32k():
+    # GQA 32/8, d128, n32768, int8:64 with 1% outlier
+    # channels x8, head-major contiguous, splits swept
+    b = build(Case(1, 32, 8, 128, 32768, R.FMT_INT8, 64, R.ORD_HEAD, 0, seed=1, outliers=True))
+    for splits in (1, 8, 64):
+        for unroll, warps in ((2, 4), (4, 8)):
+            check(b, run(b, splits, unroll=unroll, warps=warps), f"S={splits} u{unroll} w{warps}")
+    # accuracy against the exact fp32 attention stays near the calibrated budget
+    # against exact fp32 attention the error is the quantizer's, as the
+    # oracle's own dequantised reference shows
+    exact = O.reference_attention(b.q_host, b.K, b.V)
+    err_exact = O.rel_l2(run(b, 64), exact)
+    err_quant = O.rel_l2(reference(b), exact)
+    say(f"  err_exact int8:64 with outliers = {err_exact:.4g} (quantizer alone {err_quant:.4g})")
+    assert abs(err_exact - err_quant) < 0.02 * err_quant
+
+
+def test_north_star_f16_32k():
+    b = build(Case(1, 32, 8, 128, 32768, R.FMT_F16, 0, R.ORD_HEAD, 0, seed=1))
+    for splits in (1, 64):
+        check(b, run(b, splits), f"S={splits}")
+
+
+def test_long_context_int4_64k():
+    # n65536, int4:32, head-major contiguous, splits 8..256
+    b = build(Case(1, 32, 8, 128, 65536, R.FMT_INT4, 32, R.ORD_HEAD, 0, seed=1))
+    for splits in (8, 256):
+        check(b, run(b, splits), f"S={splits}")
+
+
+def test_varlen_pool_f16_qo():
+    # BASELINE configs[2] (scaled down): variable lengths from a shared,
+    # shuffled block pool, paged:16 token-major, int8:64, f16 query/output
+    B, H, Hkv, D = 4, 32, 8, 128
+    lens = O.varlen_lengths(B, 200, 900, 2)
+    n_max = int(lens.max())
+    q, K, V = O.make_data(B, H, Hkv, D, n_max, 1)
+    q16 = q.astype(np.float16)
+    kd, km, kdeq = O.quantize(R.FMT_INT8, 64, D, K)
+    vd, vm, vdeq = O.quantize(R.FMT_INT8, 64, D, V)
+    table, mb = O.pool_table(lens, 16, 512, 18)
+    dev = torch.device("cuda:0")
+    tbl = torch.from_numpy(np.where(table < 0, 0, table).astype(np.int32)).to(dev)
+    rows = 512 * Hkv * 16
+    kc = torch.zeros(rows * D, dtype=torch.uint8, device=dev)
+    vc = torch.zeros(rows * D, dtype=torch.uint8, device=dev)
+    kmc = torch.zeros(rows * 2, dtype=torch.int32, device=dev)
+    vmc = torch.zeros(rows * 2, dtype=torch.int32, device=dev)
+    # each sequence appends only its own tokens into its own pages
+    for bb in range(B):
+        L = int(lens[bb])
+        for src, dst, dm in ((K, kc, kmc), (V, vc, vmc)):
+            x = torch.from_numpy(np.ascontiguousarray(src[bb, :, :L])).to(dev)
+            R.quantize_place(R.FMT_INT8, 64, D, x, 1, Hkv, L, R.ORD_TOKEN, 16, tbl[bb], mb,
+                             dst, dm)
+    torch.cuda.synchronize()
+    q16d = torch.from_numpy(q16).to(dev)
+    out16 = torch.zeros((B, H, D), dtype=torch.float16, device=dev)
+    qdummy = torch.zeros((B, H, D), dtype=torch.float32, device=dev)
+    outdummy = torch.zeros((B, H, D), dtype=torch.float32, device=dev)
+    lens_d = torch.from_numpy(lens).to(dev)
+    ref = O.reference_attention_varlen(q16.astype(np.float32), kdeq, vdeq, lens)
+    for splits in (1, 8):
+        po = torch.zeros((B, H, splits, D), device=dev)
+        pm = torch.zeros((B, H, splits, 2), device=dev)
+        a = R.make_args(qdummy, kc, vc, kmc, vmc, tbl, outdummy, po, pm, B, H, Hkv, n_max,
+                        splits, 4, group=64, block_tokens=16, max_blocks=mb, D=D)
+        R.launch_varlen("int8_tm_p_g4_u2_d128", a, lens_d, q16=q16d, out16=out16)
+        torch.cuda.synchronize()
+        got = out16.float().cpu().numpy()
+        err = O.rel_l2(got, ref)
+        say(f"  varlen S={splits}: rel_l2={err:.3g}")
+        assert err < REL_TOL
+
+
+def test_bad_arguments_are_rejected():
+    b = build(Case(1, 8, 2, 128, 64, R.FMT_INT8, 64, R.ORD_HEAD, 0), check_cache=False)
+    a = args(b, 1, 4)
+    a.warps = 3
+    assert R.hip_lib().kvf_launch_variant(b"int8_hm_c_g4_u2_d128", a, None) == R.HIP_ERROR_INVALID_VALUE
+    a.warps = 4
+    assert R.hip_lib().kvf_launch_variant(b"int8_hm_c_g4_u2_d96", a, None) == R.HIP_ERROR_NOT_FOUND
+    a.group_shift = 4
+    assert R.hip_lib().kvf_launch_variant(b"int8_hm_c_g4_u2_d128", a, None) == R.HIP_ERROR_INVALID_VALUE
