@@ -103,10 +103,31 @@ hipError_t kvf_launch_varlen_variant(const char *variant_id, const kvf_args_t *a
                                      const kvf_varlen_args_t *va,
                                      hipStream_t stream);
 
+/* One decode step in a single kernel launch: the last workgroup of each
+ * (sequence, head group) merges the splits, which removes the reference's
+ * second (merge) launch (runtime/kvf_kernels.cuh:315-318). `counters` is
+ * caller-owned device memory of B * (pack > 1 ? Hkv : H) unsigned ints, zero
+ * before the first call; every call leaves it zero again. Calls that run
+ * concurrently (on different streams) need distinct counters, exactly as
+ * they need distinct part_o / part_ml. `va` may be NULL. Outputs match
+ * kvf_launch_variant to rounding. */
+hipError_t kvf_launch_fused_variant(const char *variant_id, const kvf_args_t *a,
+                                    const kvf_varlen_args_t *va, unsigned *counters,
+                                    hipStream_t stream);
+
 /* Only the partial (split) kernel of a variant, writing part_o / part_ml
  * even when splits == 1; for measuring the streaming kernel by itself. */
 hipError_t kvf_launch_partial_variant(const char *variant_id, const kvf_args_t *a,
                                       hipStream_t stream);
+
+/* As kvf_launch_partial_variant, with `start` and `stop` (created by the
+ * caller with timing enabled) bound to the split kernel's own dispatch, so
+ * hipEventElapsedTime(start, stop) is that kernel's execution time, the
+ * figure a kernel trace reports. Harness use (the reference's time_launch,
+ * runtime/kvf_host.h:302-331, brackets the launch with events instead). */
+hipError_t kvf_launch_partial_variant_timed(const char *variant_id, const kvf_args_t *a,
+                                            hipStream_t stream, hipEvent_t start,
+                                            hipEvent_t stop);
 
 /* Only the log-sum-exp merge (runtime/kvf_kernels.cuh:288-306) of the
  * partials named by `a` (B, H, splits, part_o, part_ml, out) for head

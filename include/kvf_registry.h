@@ -7,6 +7,11 @@
  *
  * LaunchFn takes `const Args &`, a C++ reference: this is an intra-C++
  * interface, exactly as in the reference. The C-ABI face is kvf_abi.h.
+ *
+ * Beside the reference's add(id, fn) a variant may also register its
+ * extended launcher (variable lengths, binary16 q/out, fused merge, split
+ * kernel only, kernel-bound timing events); the C-ABI entry points other than
+ * kvf_launch_variant go through it.
  */
 #ifndef KVF_REGISTRY_H
 #define KVF_REGISTRY_H
@@ -17,15 +22,30 @@
 #include <unordered_map>
 
 namespace kvf {
+namespace gfx950 {
+struct Ext;
+struct Launch;
+} /* namespace gfx950 */
 
 using LaunchFn = hipError_t (*)(const Args &, hipStream_t);
+using LaunchXFn = hipError_t (*)(const Args &, const gfx950::Ext &, const gfx950::Launch &,
+                                 hipStream_t);
 
 struct Registry {
-  std::unordered_map<std::string, LaunchFn> fn;
-  void add(const char *id, LaunchFn f) { fn[id] = f; }
+  struct Entry {
+    LaunchFn fn = nullptr;
+    LaunchXFn xfn = nullptr;
+  };
+  std::unordered_map<std::string, Entry> fn;
+  void add(const char *id, LaunchFn f) { fn[id].fn = f; }
+  void add(const char *id, LaunchFn f, LaunchXFn x) { fn[id] = Entry{f, x}; }
   LaunchFn find(const std::string &id) const {
     const auto it = fn.find(id);
-    return it == fn.end() ? nullptr : it->second;
+    return it == fn.end() ? nullptr : it->second.fn;
+  }
+  LaunchXFn findx(const std::string &id) const {
+    const auto it = fn.find(id);
+    return it == fn.end() ? nullptr : it->second.xfn;
   }
 };
 

@@ -1,0 +1,40 @@
+// kvf_ext.hpp - what travels beside kvf::Args into the gfx950 kernels, and the
+// extended launcher every dispatch variant provides.
+//
+// Args stays byte-identical to the reference's (runtime/kvf_kernels.cuh:29-46);
+// the variable-length / binary16 / fused-merge extension and the launch mode
+// (split kernel only, kernel-bound timing events) are passed separately.
+#pragma once
+
+#include "kvf_abi.h"
+
+#include <hip/hip_runtime.h>
+
+namespace kvf {
+namespace gfx950 {
+
+// Extension fields beside Args; all null by default.
+struct Ext {
+  const int *seq_lens = nullptr; // per-sequence lengths (Args::n is the maximum)
+  const _Float16 *q16 = nullptr; // binary16 query instead of Args::q
+  _Float16 *out16 = nullptr;     // binary16 output instead of Args::out
+  unsigned *counters = nullptr;  // [B][grid.y] split counters: fused merge
+};
+
+// How a decode step is enqueued: the split kernel alone (partial_only), and
+// optionally with HIP events bound to the split kernel's own dispatch
+// (hipExtLaunchKernelGGL), which time the kernel itself rather than the
+// stream around it.
+struct Launch {
+  bool partial_only = false;
+  hipEvent_t ev_start = nullptr;
+  hipEvent_t ev_stop = nullptr;
+};
+
+// Extended launcher of one variant (defined in kvf_kernels.hpp, explicitly
+// instantiated per variant by the generated kvf_inst_*.hip files).
+template <int FMT, int D, int G, int U, int ORD, bool PAGED>
+hipError_t launch_ext(const Args &a, const Ext &x, const Launch &l, hipStream_t st);
+
+} // namespace gfx950
+} // namespace kvf

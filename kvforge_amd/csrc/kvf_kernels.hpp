@@ -3,414 +3,636 @@
 // One decode step for one layer: a single query vector per head attends to n
 // cached tokens, reading every cached byte once. Functionally this is the
 // reference's decode_partial / decode_merge (runtime/kvf_kernels.cuh:124-306);
-// the mapping onto CDNA4 is this file's own:
+// the mapping onto CDNA4 is this file's own.
 //
-//   * A 64-lane wavefront consumes 16-token tiles. Lane l sits in lane-row
-//     r = l/16 at column c = l%16.
-//   * QK^T is an MFMA contraction over the head dimension with the K tile as
-//     operand A (token = column c) and the query as operand B (query head =
-//     c mod G, every head replicated 16/G times). The 16x16 result leaves in
-//     lane l the scores of tokens 4r..4r+3 for query head c mod G.
-//   * That is exactly the A-operand layout of the PV MFMA (head = c, tokens
-//     4r+j), so softmax weights go from the first MFMA to the second with no
-//     cross-lane movement. V is loaded so that lane l holds tokens 4r..4r+3
-//     of column block c, which is exactly PV's B operand.
-//   * Quantized K feeds the MFMA as exact binary16 codes; each quantization
-//     group accumulates separately and its (scale, zero) is applied to the
-//     16x16 fp32 result, so scores are fp32-exact up to summation order. The
-//     query enters as a binary16 hi/lo pair (two MFMAs), ~22 bits.
-//   * V is dequantized to binary16 with one fused multiply-add per element
-//     pair (v_pk_fma_f16); softmax weights enter PV as a binary16 hi/lo pair.
-//   * Online softmax keeps one running max per head for the whole wave and
-//     only rescales when a score exceeds it by more than TAU (log2 units): a
-//     wave-uniform, rarely taken branch. The exact max is tracked beside it,
-//     so partials report the true max as the reference does.
-//   * Loads are issued U tiles ahead (nontemporal, 4-16 B per lane); paged
-//     tiles never straddle a page (16 | page size), so the block-table lookup
-//     is one scalar load per tile.
-//   * Waves of a workgroup combine through LDS; splits combine in
-//     decode_merge (log-sum-exp), or the workgroup writes the normalised
-//     output directly when splits == 1.
+// Work unit: a 64-lane wavefront consumes 32-token tiles made of two 16-token
+// sub-tiles (tiles are aligned to absolute token positions, so a sub-tile
+// never straddles a page of >= 16 tokens). Lane l sits in lane-row r = l/16
+// at column c = l%16.
+//
+// QK^T: per sub-tile, a 16x16x32 binary16 MFMA chain with the K sub-tile as
+// operand A (token = MFMA row: lane (r,c) loads token c) and the query as
+// operand B. MFMA columns are (quantisation group, query head) pairs: a
+// column carries its head's query restricted to the dims of its group, so
+// one accumulator yields per-group partial dots; each lane applies its own
+// group's (scale, zero) and a DPP row rotation sums the columns of a head.
+// The query enters as a binary16 hi/lo pair (~22 bits). When the pairs fill
+// at most 8 columns the hi half sits in columns 0-7 and the lo half in 8-15,
+// so one MFMA yields both; otherwise hi and lo are two MFMAs.
+//
+// Quantized codes enter the MFMAs as binary16 subnormals (code * 2^-24),
+// built by one v_perm per two codes; gfx950 MFMAs keep subnormal inputs, so
+// the products are exact. Scores of quantized formats are kept in units of
+// 2^-24 and the factor is folded into the exp2 argument.
+//
+// PV: one 16x16x32 MFMA per 16 output dims and tile, the softmax weights as
+// operand A (rows = the same (group, head) pairs, hi/lo split like the
+// query), V codes as operand B (MFMA k = the 32 tokens of the tile). The V
+// scale of a token and group is folded into that row's weight and the zero
+// point into a per-row running sum, so V is never dequantised element by
+// element; each lane keeps the rows whose group matches its V dims.
+//
+// Streaming: every wave keeps a ring of DEPTH tiles; tile k+DEPTH-1 is
+// issued before tile k is consumed. Loads are raw buffer loads through
+// per-sub-tile descriptors built in scalar registers: the record count
+// stops the loads at the sequence end, and a tile outside the wave's range
+// gets zero-length descriptors whose loads return zeros without touching
+// memory, so the load stream is unconditional and the compiler's wait counts
+// are static. The first DEPTH-1 tiles are issued before the query is
+// converted, so the two latencies overlap.
+//
+// Online softmax keeps one running max per head for the whole wave and only
+// rescales when a score exceeds it by more than TAU (log2 units): a
+// wave-uniform, rarely taken branch. The exact max is tracked beside it, so
+// partials report the true max as the reference does. Waves of a workgroup
+// combine through LDS; splits combine in decode_merge (log-sum-exp), in the
+// last workgroup of a head group when the caller supplies merge counters, or
+// the workgroup writes the normalised output directly when splits == 1.
 #pragma once
 
 #include "kvf_abi.h"
+#include "kvf_ext.hpp"
 #include "kvf_registry.h"
 
+#include <hip/hip_ext.h>
 #include <hip/hip_runtime.h>
 #include <stdint.h>
+#include <algorithm>
+#include <type_traits>
 
 namespace kvf {
 namespace gfx950 {
 
 typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
-typedef _Float16 half4_t __attribute__((ext_vector_type(4)));
 typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
 typedef float float4_t __attribute__((ext_vector_type(4)));
-typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
+typedef int32_t i32x2_t __attribute__((ext_vector_type(2)));
+typedef int32_t i32x4_t __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
 
-constexpr int TILE = 16;       // tokens per wavefront step
-constexpr float TAU = 8.0f;    // rescale threshold, log2 units
-constexpr uint32_t MAGIC = 0x64646464u; // byte 0x64 -> binary16 1024 + b
+constexpr int SUB = 16;                  // tokens per sub-tile (MFMA rows)
+constexpr int TT = 32;                   // tokens per tile (PV MFMA k)
+constexpr float TAU = 8.0f;              // rescale threshold, log2 units
+constexpr float CODE_SCALE = 16777216.f; // 2^24: undoes the subnormal encoding
+constexpr int RSRC_WORD3 = 0x00020000;   // gfx9 raw buffer: 32-bit data format
+constexpr int CPOL_NT = 2;               // nontemporal: every byte is used once
 
 template <int FMT> constexpr int bits_of() {
   return FMT == FMT_F16 ? 16 : FMT == FMT_INT8 ? 8 : 4;
 }
 
-// Lane geometry of one (format, head dimension, quantization group).
-template <int FMT, int D, int GQ> struct Geo {
+// Tiles kept in flight per wave for the reference's unroll knob U.
+template <int U> constexpr int depth_of() { return U == 2 ? 2 : 3; }
+
+// Lane geometry of one (format, head dim, quantisation group, pack size).
+template <int FMT, int D, int GQ, int G> struct Geo {
   static constexpr int BITS = bits_of<FMT>();
-  static constexpr int ROW = D * BITS / 8;                 // bytes per cached row
-  static constexpr int GRP = FMT == FMT_F16 ? D : GQ;      // elements per scale group
-  // QK side: a "piece" is one load per lane; the four lane-rows of a piece
-  // cover 4*W consecutive bytes of each of the 16 tokens, inside one group.
-  static constexpr int W = FMT == FMT_F16 ? 16 : (GRP * BITS / 32 < 16 ? GRP * BITS / 32 : 16);
-  static constexpr int P = ROW / (4 * W);                  // pieces per row
-  static constexpr int EP = W * 8 / BITS;                  // elements per lane per piece
-  static constexpr int SPP = EP / 8;                       // x32 MFMA steps per piece
-  static constexpr int KSTEPS = P * SPP;                   // = D / 32
-  static constexpr int NG = D / GRP;                       // scale groups per row
-  // PV side: lane holds EV elements (one column block) of 4 tokens.
+  static constexpr bool QUANT = FMT != FMT_F16;
+  static constexpr int ROW = D * BITS / 8;            // bytes per cached row
+  static constexpr int GRP = QUANT ? GQ : D;          // elements per scale group
+  static constexpr int NG = D / GRP;                  // scale groups per row
+  static constexpr int COLS = G * NG;                 // (group, head) pairs
+  static constexpr bool HL = COLS <= 8;               // hi/lo share one MFMA
+  static constexpr int PASSES = COLS > 16 ? 2 : 1;
+  // K: lane-row r loads CH bytes at r*CH + j*4*CH of its token's row.
+  static constexpr int CH = ROW / 4 < 16 ? ROW / 4 : 16;
+  static constexpr int NCH = ROW / (4 * CH);
+  static constexpr int SPC = CH * 8 / BITS / 8;       // MFMA k-steps per chunk
+  static constexpr int KSTEPS = NCH * SPC;            // = D / 32
+  // V: lane column c owns dims [c*EV, c*EV+EV) of 8 tokens.
   static constexpr int EV = D / 16;
-  static constexpr int WV = EV * BITS / 8;                 // bytes per token per lane
-  static constexpr int WVW = WV >= 4 ? WV / 4 : 1;         // 32-bit words per token
-  static constexpr int MW = NG;                            // meta words per row
+  static constexpr int VB = EV * BITS / 8;            // bytes per token per lane
+  static constexpr int VW = VB >= 4 ? VB / 4 : 1;     // 32-bit words per token
+  // G >= 4: the 4 columns of a quad share a group, so lane (r, c) loads the
+  // whole meta row of token 4r + c%4 and a quad broadcast hands it around
+  static constexpr bool QMETA = QUANT && G >= 4;
   static_assert(D == 64 || D == 128, "head dimension");
-  static_assert(KSTEPS == D / 32, "piece geometry");
-  static_assert(P * 4 * W == ROW, "pieces tile the row");
+  static_assert(G == 1 || G == 2 || G == 4 || G == 8, "pack size");
+  static_assert(KSTEPS * 32 == D, "chunk geometry");
+  static_assert(NCH * 4 * CH == ROW, "chunks tile the row");
+  static_assert(!QUANT || (GQ >= 32 && GQ <= D), "group");
+  static_assert(COLS <= 32, "at most two column passes");
 };
 
 __device__ __forceinline__ uint32_t perm(uint32_t s0, uint32_t s1, uint32_t sel) {
   return __builtin_amdgcn_perm(s0, s1, sel);
 }
-
 __device__ __forceinline__ half2_t as_h2(uint32_t w) { return __builtin_bit_cast(half2_t, w); }
-__device__ __forceinline__ uint32_t as_u(half2_t h) { return __builtin_bit_cast(uint32_t, h); }
+__device__ __forceinline__ float lo_f(uint32_t w) { return (float)as_h2(w).x; }
+__device__ __forceinline__ float hi_f(uint32_t w) { return (float)as_h2(w).y; }
 
-// Streaming loads of NB bytes (every K/V byte is used once).
+// byte k of s1 and byte k of s0, each zero-extended to 16 bits:
+// two codes as binary16 subnormals (code * 2^-24)
+__device__ __host__ constexpr uint32_t sel_pair(int k) {
+  return 0x0c000c00u | ((uint32_t)(4 + k) << 16) | (uint32_t)k;
+}
+
+// Rotation by N lanes inside each row of 16 (DPP row_ror).
+template <int N> __device__ __forceinline__ float ror16(float x) {
+  static_assert(N >= 1 && N <= 15, "rotation");
+  return __builtin_bit_cast(
+      float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), 0x120 + N, 0xF, 0xF, false));
+}
+
+// Sum of x over the columns c' == c (mod G) of the lane's row of 16.
+template <int G> __device__ __forceinline__ float sum_head_cols(float x) {
+  if constexpr (G <= 1) x += ror16<1>(x);
+  if constexpr (G <= 2) x += ror16<2>(x);
+  if constexpr (G <= 4) x += ror16<4>(x);
+  if constexpr (G <= 8) x += ror16<8>(x);
+  return x;
+}
+
+// Raw buffer loads of NB bytes at voffset through descriptor `rs`.
 template <int NB> struct Raw { uint32_t w[NB >= 4 ? NB / 4 : 1]; };
 
 template <int NB>
-__device__ __forceinline__ void load_stream(const unsigned char *p, Raw<NB> &r) {
+__device__ __forceinline__ void bload(__amdgpu_buffer_rsrc_t rs, int voff, Raw<NB> &r) {
   if constexpr (NB == 16) {
-    const u32x4_t v = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t *>(p));
+    const i32x4_t v = __builtin_amdgcn_raw_buffer_load_b128(rs, voff, 0, CPOL_NT);
     r.w[0] = v.x; r.w[1] = v.y; r.w[2] = v.z; r.w[3] = v.w;
   } else if constexpr (NB == 8) {
-    const u32x2_t v = __builtin_nontemporal_load(reinterpret_cast<const u32x2_t *>(p));
+    const i32x2_t v = __builtin_amdgcn_raw_buffer_load_b64(rs, voff, 0, CPOL_NT);
     r.w[0] = v.x; r.w[1] = v.y;
   } else if constexpr (NB == 4) {
-    r.w[0] = __builtin_nontemporal_load(reinterpret_cast<const uint32_t *>(p));
+    r.w[0] = __builtin_amdgcn_raw_buffer_load_b32(rs, voff, 0, CPOL_NT);
   } else {
     static_assert(NB == 2, "load width");
-    r.w[0] = __builtin_nontemporal_load(reinterpret_cast<const uint16_t *>(p));
+    r.w[0] = (uint16_t)__builtin_amdgcn_raw_buffer_load_b16(rs, voff, 0, CPOL_NT);
   }
 }
 
-// Order in which a lane's converted binary16 values hold its elements, per
-// 32-bit word of packed codes. int4 splits even and odd nibbles.
+// Buffer descriptor over [base + off, base + off + bytes). Every field is
+// wave-uniform by construction; readfirstlane makes that explicit so the
+// descriptor lives in scalar registers (a descriptor the compiler believes
+// divergent would wrap every load in a waterfall loop).
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t rsrc(const void *base, long long off,
+                                                       uint32_t bytes) {
+  const uint64_t p = reinterpret_cast<uint64_t>(base) + (uint64_t)off;
+  const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)p);
+  const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(p >> 32));
+  const uint32_t n = __builtin_amdgcn_readfirstlane(bytes);
+  void *ptr = reinterpret_cast<void *>(((uint64_t)hi << 32) | lo);
+  return __builtin_amdgcn_make_buffer_rsrc(ptr, 0, (int)n, RSRC_WORD3);
+}
+
+// Order in which a lane's binary16 values hold the 8 elements of one k-step.
+// int4 splits even and odd nibbles.
 template <int FMT> __device__ __host__ constexpr int slot_elem(int i) {
-  if constexpr (FMT == FMT_INT4) {
-    constexpr int ord[8] = {0, 2, 4, 6, 1, 3, 5, 7};
-    return (i / 8) * 8 + ord[i % 8];
-  } else {
-    return i;
-  }
+  if constexpr (FMT == FMT_INT4) return i < 4 ? 2 * i : 2 * i - 7; // 0 2 4 6 1 3 5 7
+  else return i;
 }
 
-// Raw K words of one piece -> binary16 A-operand values (exact for codes).
-template <int FMT, int EP>
-__device__ __forceinline__ void k_to_half(const uint32_t *w, uint32_t (&h)[EP / 2]) {
-  const half2_t k1024 = {(_Float16)1024.0f, (_Float16)1024.0f};
-  if constexpr (FMT == FMT_F16) {
-#pragma unroll
-    for (int i = 0; i < EP / 2; ++i) h[i] = w[i];
-  } else if constexpr (FMT == FMT_INT8) {
-#pragma unroll
-    for (int i = 0; i < EP / 4; ++i) {
-      h[2 * i] = as_u(as_h2(perm(MAGIC, w[i], 0x04010400u)) - k1024);
-      h[2 * i + 1] = as_u(as_h2(perm(MAGIC, w[i], 0x04030402u)) - k1024);
-    }
-  } else {
-#pragma unroll
-    for (int i = 0; i < EP / 8; ++i) {
-      const uint32_t lo = w[i] & 0x0F0F0F0Fu;
-      const uint32_t hi = (w[i] >> 4) & 0x0F0F0F0Fu;
-      h[4 * i + 0] = as_u(as_h2(perm(MAGIC, lo, 0x04010400u)) - k1024);
-      h[4 * i + 1] = as_u(as_h2(perm(MAGIC, lo, 0x04030402u)) - k1024);
-      h[4 * i + 2] = as_u(as_h2(perm(MAGIC, hi, 0x04010400u)) - k1024);
-      h[4 * i + 3] = as_u(as_h2(perm(MAGIC, hi, 0x04030402u)) - k1024);
-    }
-  }
-}
-
-// Element e of tokens A and B of a lane's V column block, as a binary16 pair
-// (A low, B high), dequantised with the pair's (scale, zero).
-template <int FMT, int EV>
-__device__ __forceinline__ uint32_t v_pair(const uint32_t *ta, const uint32_t *tb, int e,
-                                           half2_t sc, half2_t z) {
-  if constexpr (FMT == FMT_F16) {
-    return perm(tb[e / 2], ta[e / 2], (e & 1) ? 0x07060302u : 0x05040100u);
-  } else {
-    const half2_t k1024 = {(_Float16)1024.0f, (_Float16)1024.0f};
-    uint32_t x;
-    if constexpr (FMT == FMT_INT8) {
-      const int k = e & 3;
-      x = perm(tb[e / 4], ta[e / 4], (k < 2) ? 0x05010400u : 0x07030602u);
-      x = perm(MAGIC, x, (k & 1) ? 0x04030402u : 0x04010400u);
-    } else {
-      // nibble e: even e are the low nibbles of byte e/2, odd e the high
-      const uint32_t a = (e & 1) ? (ta[0] >> 4) & 0x0F0F0F0Fu : ta[0] & 0x0F0F0F0Fu;
-      const uint32_t b = (e & 1) ? (tb[0] >> 4) & 0x0F0F0F0Fu : tb[0] & 0x0F0F0F0Fu;
-      const int k = (e >> 1) & 3; // byte index
-      x = perm(b, a, (k < 2) ? 0x05010400u : 0x07030602u);
-      x = perm(MAGIC, x, (k & 1) ? 0x04030402u : 0x04010400u);
-    }
-    const half2_t c = as_h2(x) - k1024;
-    return as_u(__builtin_elementwise_fma(c, sc, z));
-  }
-}
-
-// Extension fields (variable lengths, binary16 q/out); all null by default.
-struct Ext {
-  const int *seq_lens = nullptr;
-  const _Float16 *q16 = nullptr;
-  _Float16 *out16 = nullptr;
+// Loads of one tile in flight.
+template <int FMT, int D, int GQ, int G> struct TileBuf {
+  using Gm = Geo<FMT, D, GQ, G>;
+  Raw<Gm::CH> k[2][Gm::NCH];                      // sub-tile s, token c
+  Raw<Gm::VB> v[8];                               // token tau(r, i)
+  // (scale, zero) of K and V for tau(r, i), per pass; with QMETA the raw
+  // meta rows of token 4r + c%4 of each sub-tile, broadcast in compute()
+  uint32_t km[Gm::QUANT && !Gm::QMETA ? Gm::PASSES : 1][8];
+  uint32_t vm[Gm::QUANT && !Gm::QMETA ? Gm::PASSES : 1][8];
+  Raw<Gm::QMETA ? Gm::NG * 4 : 4> kmr[2], vmr[2];
 };
 
-// Row of (b, h, t) in the cache, as the reference defines it
-// (runtime/kvf_kernels.cuh:51-64). For paged layouts `page` is the page that
-// holds t (one per 16-token tile).
-template <int ORD, bool PAGED>
-__device__ __forceinline__ long long tile_row(const Args &a, int b, int h, int t, long long page) {
-  if constexpr (!PAGED) {
-    return ORD == ORD_HEAD ? ((long long)b * a.Hkv + h) * a.n + t
-                           : ((long long)b * a.n + t) * a.Hkv + h;
-  } else {
-    const int bt = 1 << a.block_shift;
-    const long long base = page * a.Hkv * bt;
-    return ORD == ORD_HEAD ? base + (long long)h * bt + (t & (bt - 1))
-                           : base + (long long)(t & (bt - 1)) * a.Hkv + h;
+// Broadcast of quad lane I's value to the whole quad (DPP quad_perm).
+template <int I> __device__ __forceinline__ uint32_t quad_bcast(uint32_t x) {
+  return (uint32_t)__builtin_amdgcn_mov_dpp((int)x, I * 0x55, 0xF, 0xF, false);
+}
+
+// Calls f(std::integral_constant<int, i>) for i = 0 .. N-1.
+template <int N, int I = 0, class F> __device__ __forceinline__ void static_for(F &&f) {
+  if constexpr (I < N) {
+    f(std::integral_constant<int, I>{});
+    static_for<N, I + 1>(f);
   }
 }
 
-template <int FMT, int D, int GQ, int U, int ORD, bool PAGED>
-__global__ void __launch_bounds__(512)
-decode_partial(const Args a, const Ext x, const int G, const int final_out) {
-  using Gm = Geo<FMT, D, GQ>;
-  constexpr int P = Gm::P, EP = Gm::EP, W = Gm::W, SPP = Gm::SPP, KSTEPS = Gm::KSTEPS;
-  constexpr int NG = Gm::NG, EV = Gm::EV, WV = Gm::WV, WVW = Gm::WVW;
-  constexpr int ROW = Gm::ROW;
+// Token of the tile held in slot i of lane-row r for the score and PV
+// layouts: sub-tile i/4, row 4r + i%4.
+__device__ __forceinline__ int tau(int r, int i) { return (i >> 2) * SUB + 4 * r + (i & 3); }
+
+template <int D, int NT>
+__device__ void merge_head(const Args &a, const Ext &x, long long head, float *lds);
+
+template <int FMT, int D, int GQ, int G, int U, int ORD, bool PAGED, int WPB>
+__global__ void __launch_bounds__(WPB * 64)
+decode_partial(const Args a, const Ext x, const int final_out) {
+  using Gm = Geo<FMT, D, GQ, G>;
+  constexpr bool QUANT = Gm::QUANT, HL = Gm::HL, QMETA = Gm::QMETA;
+  constexpr int ROW = Gm::ROW, NG = Gm::NG, COLS = Gm::COLS, PASSES = Gm::PASSES;
+  constexpr int CH = Gm::CH, NCH = Gm::NCH, SPC = Gm::SPC, KSTEPS = Gm::KSTEPS;
+  constexpr int EV = Gm::EV, VB = Gm::VB, VW = Gm::VW, GRP = Gm::GRP;
+  constexpr int DEPTH = depth_of<U>();
+  constexpr int NQ = HL ? 1 : 2;                   // query operands per k-step
+  constexpr float UNIT = QUANT ? CODE_SCALE : 1.f; // log2 units per score unit
+  constexpr float TAU_S = TAU / UNIT;
+  using Buf = TileBuf<FMT, D, GQ, G>;
 
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int nw = a.warps;
-  const int r = lane >> 4;   // lane-row
-  const int c = lane & 15;   // column
+  constexpr int nw = WPB; // equals a.warps, checked at launch
+  const int r = lane >> 4;
+  const int c = lane & 15;
 
   const int split = blockIdx.x;
   const int hb = blockIdx.y;
   const int b = blockIdx.z;
   const int gq = a.H / a.Hkv;
   const int hkv = G > 1 ? hb : hb / gq;
-  const int my_head = c % G;              // packed head index of this lane
-  const int hq_lane = G > 1 ? hkv * G + my_head : hb;
+  const int hq_lane = G > 1 ? hkv * G + (c % G) : hb;
 
   const int len = x.seq_lens ? x.seq_lens[b] : a.n;
   const int chunk = (len + a.splits - 1) / a.splits;
   const int t0 = split * chunk;
   const int t1 = min(len, t0 + chunk);
-  const int tile_first = t0 / TILE;
-  const int n_tiles = t1 > t0 ? (t1 - 1) / TILE - tile_first + 1 : 0;
+  const int tile_first = t0 / TT;
+  const int n_tiles = t1 > t0 ? (t1 - 1) / TT - tile_first + 1 : 0;
+  const int nk = wave < n_tiles ? (n_tiles - wave + nw - 1) / nw : 0; // this wave's tiles
 
-  // ---- query: binary16 hi/lo in the B-operand layout, group sums ----------
-  half8_t qhi[KSTEPS], qlo[KSTEPS];
-  float qs[NG];
+  // (group, head) pair of column c in pass p; HL packs the hi half in
+  // columns 0-7 and the lo half in 8-15, columns beyond the pairs stay zero
+  auto col_id = [&](int p) __attribute__((always_inline)) { return HL ? (c & 7) : ((p * 16 + c) % COLS); };
+  const bool col_live = HL ? (c & 7) < COLS : true;
+  const bool col_lo = HL && c >= 8;
+
+  // ---- per-lane constant offsets inside a sub-tile -----------------------------
+  const int tstride = ORD == ORD_HEAD ? 1 : a.Hkv; // rows between tokens
+  const int koff = c * tstride * ROW + r * CH;
+  int voff[4], moff[PASSES][4];
 #pragma unroll
-  for (int g = 0; g < NG; ++g) qs[g] = 0.f;
-  {
-    const long long qbase = ((long long)b * a.H + hq_lane) * D;
+  for (int i = 0; i < 4; ++i) {
+    voff[i] = (4 * r + i) * tstride * ROW + c * VB;
 #pragma unroll
-    for (int p = 0; p < P; ++p) {
-      const int d0 = p * 4 * EP + r * EP;
-      const int grp = (p * 4 * EP) / Gm::GRP;
-#pragma unroll
-      for (int m = 0; m < SPP; ++m) {
-#pragma unroll
-        for (int i = 0; i < 8; ++i) {
-          const int d = d0 + slot_elem<FMT>(8 * m + i);
-          float qv = x.q16 ? (float)x.q16[qbase + d] : a.q[qbase + d];
-          qv *= a.scale_log2;
-          const _Float16 hi = (_Float16)qv;
-          const _Float16 lo = (_Float16)(qv - (float)hi);
-          qhi[p * SPP + m][i] = hi;
-          qlo[p * SPP + m][i] = lo;
-          qs[grp] += qv;
-        }
-      }
-    }
+    for (int p = 0; p < PASSES; ++p)
+      moff[p][i] = ((4 * r + i) * tstride * NG + (col_id(p) % COLS) / G) * 4;
   }
-#pragma unroll
-  for (int g = 0; g < NG; ++g) {
-    qs[g] += __shfl_xor(qs[g], 16);
-    qs[g] += __shfl_xor(qs[g], 32);
-  }
+  const int mrow = (4 * r + (c & 3)) * tstride * NG * 4; // QMETA: meta row of token 4r + c%4
 
-  // ---- per-lane state ------------------------------------------------------
-  float4_t acc[EV];
-#pragma unroll
-  for (int e = 0; e < EV; ++e) acc[e] = (float4_t){0.f, 0.f, 0.f, 0.f};
-  float m_run = -INFINITY;  // per head, identical across the lanes of a head
-  float m_true = -INFINITY; // exact max of this lane's scores
-  float l_sum = 0.f;
-
-  const unsigned char *kbase = a.k;
-  const unsigned char *vbase = a.v;
-  const uint32_t *kmeta = reinterpret_cast<const uint32_t *>(a.k_meta);
-  const uint32_t *vmeta = reinterpret_cast<const uint32_t *>(a.v_meta);
-  const int rstride = ORD == ORD_HEAD ? 1 : a.Hkv; // rows between tokens of a tile
-  const int vgroup = (c * EV) / Gm::GRP;           // scale group of this lane's V block
-
-  const int n_iter = (n_tiles + nw * U - 1) / (nw * U);
-  for (int it = 0; it < n_iter; ++it) {
-    Raw<W> kraw[U][P];
-    Raw<WV> vraw[U][4];
-    uint32_t kmw[U][4][NG];
-    uint32_t vmw[U][4];
-    int tt[U];
-#pragma unroll
-    for (int u = 0; u < U; ++u) {
-      const int ti = wave + nw * (it * U + u);
-      tt[u] = ti < n_tiles ? (tile_first + ti) * TILE : -1;
-      if (tt[u] >= 0) {
-        const int tbase = tt[u];
-        long long page = 0;
-        if constexpr (PAGED)
-          page = a.block_table[(long long)b * a.max_blocks + (tbase >> a.block_shift)];
-        const long long row0 = tile_row<ORD, PAGED>(a, b, hkv, tbase, page);
-        const int lo_t = max(t0 - tbase, 0);
-        const int hi_t = min(t1 - tbase, TILE) - 1;
-        // K: token column c
-        const int tk = min(max(c, lo_t), hi_t);
-        const unsigned char *kp = kbase + (row0 + (long long)tk * rstride) * ROW + r * W;
-#pragma unroll
-        for (int p = 0; p < P; ++p) load_stream<W>(kp + p * 4 * W, kraw[u][p]);
-        // V and meta: tokens 4r+j
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          const int tv = min(max(4 * r + j, lo_t), hi_t);
-          const long long rowv = row0 + (long long)tv * rstride;
-          load_stream<WV>(vbase + rowv * ROW + c * WV, vraw[u][j]);
-          if constexpr (FMT != FMT_F16) {
-#pragma unroll
-            for (int g = 0; g < NG; ++g) kmw[u][j][g] = kmeta[rowv * NG + g];
-            vmw[u][j] = vmeta[rowv * NG + vgroup];
-          }
-        }
+  // ---- paged: page ids of this wave's sub-tiles, 64 per batch (lane = sub-tile)
+  int vpages = 0;
+  const int bs = a.block_shift;
+  auto load_pages = [&](int kb32) __attribute__((always_inline)) {
+    if constexpr (PAGED) {
+      const int kk = kb32 + (lane >> 1);
+      const int ti = wave + nw * kk;
+      int pg = 0;
+      if (kk < nk && ti < n_tiles) {
+        const int t = (tile_first + ti) * TT + (lane & 1) * SUB;
+        if (t < len) pg = a.block_table[(long long)b * a.max_blocks + (t >> bs)];
       }
+      vpages = pg;
     }
+  };
+  load_pages(0);
 
+  // ---- issue all loads of wave-tile k into buf ---------------------------------
+  auto issue = [&](Buf &buf, int k) __attribute__((always_inline)) {
+    const bool live = k >= 0 && k < nk;
+    const int tbase = (tile_first + wave + nw * k) * TT;
 #pragma unroll
-    for (int u = 0; u < U; ++u) {
-      if (tt[u] < 0) continue; // wave-uniform
-      const int tbase = tt[u];
-      // ---- scores --------------------------------------------------------
-      float4_t cg[NG];
+    for (int s = 0; s < 2; ++s) {
+      const int ts = tbase + s * SUB;
+      long long row0;
+      if constexpr (!PAGED) {
+        row0 = ORD == ORD_HEAD ? ((long long)b * a.Hkv + hkv) * a.n + ts
+                               : ((long long)b * a.n + ts) * a.Hkv + hkv;
+      } else {
+        if (s == 0 && (k & 31) == 0 && k > 0) load_pages(k);
+        const long long page = live ? __builtin_amdgcn_readlane(vpages, 2 * (k & 31) + s) : 0;
+        const int bt = 1 << bs;
+        const long long base = page * a.Hkv * bt;
+        row0 = ORD == ORD_HEAD ? base + (long long)hkv * bt + (ts & (bt - 1))
+                               : base + (long long)(ts & (bt - 1)) * a.Hkv + hkv;
+      }
+      // tokens this sub-tile may read: up to the sequence end
+      const int nv = live ? min(SUB, max(0, len - ts)) : 0;
+      const uint32_t dbytes = nv > 0 ? (uint32_t)((nv - 1) * tstride * ROW + ROW) : 0u;
+      const auto rk = rsrc(a.k, row0 * ROW, dbytes);
+      const auto rv = rsrc(a.v, row0 * ROW, dbytes);
 #pragma unroll
-      for (int g = 0; g < NG; ++g) cg[g] = (float4_t){0.f, 0.f, 0.f, 0.f};
+      for (int j = 0; j < NCH; ++j) bload<CH>(rk, koff + j * 4 * CH, buf.k[s][j]);
 #pragma unroll
-      for (int p = 0; p < P; ++p) {
-        uint32_t hk[EP / 2];
-        k_to_half<FMT, EP>(kraw[u][p].w, hk);
-        const int grp = (p * 4 * EP) / Gm::GRP;
+      for (int i = 0; i < 4; ++i) bload<VB>(rv, voff[i], buf.v[4 * s + i]);
+      if constexpr (QUANT) {
+        const uint32_t mbytes = nv > 0 ? (uint32_t)(((nv - 1) * tstride + 1) * NG * 4) : 0u;
+        const auto rkm = rsrc(a.k_meta, row0 * NG * 4, mbytes);
+        const auto rvm = rsrc(a.v_meta, row0 * NG * 4, mbytes);
+        if constexpr (QMETA) {
+          bload<NG * 4>(rkm, mrow, buf.kmr[s]);
+          bload<NG * 4>(rvm, mrow, buf.vmr[s]);
+        } else
 #pragma unroll
-        for (int m = 0; m < SPP; ++m) {
-          half8_t av;
+        for (int p = 0; p < PASSES; ++p)
 #pragma unroll
           for (int i = 0; i < 4; ++i) {
-            const half2_t h2 = as_h2(hk[4 * m + i]);
-            av[2 * i] = h2.x;
-            av[2 * i + 1] = h2.y;
+            Raw<4> t;
+            bload<4>(rkm, moff[p][i], t);
+            buf.km[p][4 * s + i] = t.w[0];
+            bload<4>(rvm, moff[p][i], t);
+            buf.vm[p][4 * s + i] = t.w[0];
           }
-          cg[grp] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av, qhi[p * SPP + m], cg[grp], 0, 0, 0);
-          cg[grp] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av, qlo[p * SPP + m], cg[grp], 0, 0, 0);
-        }
-      }
-      float s[4];
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        float v;
-        if constexpr (FMT == FMT_F16) {
-          v = cg[0][j];
-        } else {
-          v = 0.f;
-#pragma unroll
-          for (int g = 0; g < NG; ++g) {
-            const half2_t mz = as_h2(kmw[u][j][g]);
-            v = fmaf((float)mz.x, cg[g][j], v);
-            v = fmaf((float)mz.y, qs[g], v);
-          }
-        }
-        const int t = tbase + 4 * r + j;
-        s[j] = (t >= t0 && t < t1) ? v : -INFINITY;
-      }
-      // ---- online softmax --------------------------------------------------
-      const float tmax = fmaxf(fmaxf(s[0], s[1]), fmaxf(s[2], s[3]));
-      m_true = fmaxf(m_true, tmax);
-      if (__any(tmax > m_run + TAU)) { // wave-uniform, rare after the first tile
-        float cand = fmaxf(m_run, tmax);
-        for (int mask = G; mask < 64; mask <<= 1) cand = fmaxf(cand, __shfl_xor(cand, mask));
-        const float alpha = cand == -INFINITY ? 1.f : exp2f(m_run - cand);
-        l_sum *= alpha;
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          const float aj = __shfl(alpha, 16 * r + ((4 * r + j) % 16));
-#pragma unroll
-          for (int e = 0; e < EV; ++e) acc[e][j] *= aj;
-        }
-        m_run = cand;
-      }
-      float pj[4];
-#pragma unroll
-      for (int j = 0; j < 4; ++j) pj[j] = exp2f(s[j] - m_run);
-      l_sum += (pj[0] + pj[1]) + (pj[2] + pj[3]);
-      // weights as a binary16 hi/lo pair: PV then sees ~22-bit weights
-      half4_t pa, pb;
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        pa[j] = (_Float16)pj[j];
-        pb[j] = (_Float16)(pj[j] - (float)pa[j]);
-      }
-      // ---- values ------------------------------------------------------------
-      half2_t sc01 = {(_Float16)1.f, (_Float16)1.f}, z01 = {(_Float16)0.f, (_Float16)0.f};
-      half2_t sc23 = sc01, z23 = z01;
-      if constexpr (FMT != FMT_F16) {
-        sc01 = as_h2(perm(vmw[u][1], vmw[u][0], 0x05040100u));
-        z01 = as_h2(perm(vmw[u][1], vmw[u][0], 0x07060302u));
-        sc23 = as_h2(perm(vmw[u][3], vmw[u][2], 0x05040100u));
-        z23 = as_h2(perm(vmw[u][3], vmw[u][2], 0x07060302u));
-      }
-      // tokens outside [t0, t1) carry weight 0; zero their values too so a
-      // non-finite cache entry cannot turn 0 * inf into NaN
-      uint32_t vw[4][WVW];
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const bool ok = s[j] != -INFINITY;
-#pragma unroll
-        for (int w = 0; w < WVW; ++w) vw[j][w] = ok ? vraw[u][j].w[w] : 0u;
-      }
-#pragma unroll
-      for (int e = 0; e < EV; ++e) {
-        const uint32_t b01 = v_pair<FMT, EV>(vw[0], vw[1], e, sc01, z01);
-        const uint32_t b23 = v_pair<FMT, EV>(vw[2], vw[3], e, sc23, z23);
-        half4_t bv;
-        bv[0] = as_h2(b01).x;
-        bv[1] = as_h2(b01).y;
-        bv[2] = as_h2(b23).x;
-        bv[3] = as_h2(b23).y;
-        acc[e] = __builtin_amdgcn_mfma_f32_16x16x16f16(pa, bv, acc[e], 0, 0, 0);
-        acc[e] = __builtin_amdgcn_mfma_f32_16x16x16f16(pb, bv, acc[e], 0, 0, 0);
       }
     }
+  };
+
+  // ---- query loads, then the first DEPTH-1 tiles under them ------------------------
+  // The ring is three named buffers picked by compile-time index, so every
+  // access has a constant address and the buffers stay in registers.
+  Buf buf0, buf1, buf2;
+  auto ring = [&](auto I) __attribute__((always_inline)) -> Buf & {
+    constexpr int i = decltype(I)::value;
+    if constexpr (i == 0) return buf0;
+    else if constexpr (i == 1) return buf1;
+    else return buf2;
+  };
+  float raw[KSTEPS][8];
+  {
+    const long long qbase = ((long long)b * a.H + hq_lane) * D;
+    if (x.q16) {
+#pragma unroll
+      for (int j = 0; j < NCH; ++j)
+#pragma unroll
+        for (int m = 0; m < SPC; ++m) {
+          const int d0 = (j * 4 * CH + r * CH) * 8 / Gm::BITS + 8 * m;
+          const half8_t h = *reinterpret_cast<const half8_t *>(x.q16 + qbase + d0);
+#pragma unroll
+          for (int i = 0; i < 8; ++i) raw[j * SPC + m][i] = (float)h[i];
+        }
+    } else {
+#pragma unroll
+      for (int j = 0; j < NCH; ++j)
+#pragma unroll
+        for (int m = 0; m < SPC; ++m) {
+          const int d0 = (j * 4 * CH + r * CH) * 8 / Gm::BITS + 8 * m;
+          const float4_t f0 = *reinterpret_cast<const float4_t *>(a.q + qbase + d0);
+          const float4_t f1 = *reinterpret_cast<const float4_t *>(a.q + qbase + d0 + 4);
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            raw[j * SPC + m][i] = f0[i];
+            raw[j * SPC + m][4 + i] = f1[i];
+          }
+        }
+    }
+  }
+  static_for<DEPTH - 1>([&](auto Ui) __attribute__((always_inline)) {
+    __builtin_amdgcn_sched_barrier(0);
+    issue(ring(Ui), decltype(Ui)::value);
+  });
+  __builtin_amdgcn_sched_barrier(0);
+
+  // ---- query: binary16 hi/lo B operands, zero outside the column's group ----
+  half8_t qb[PASSES][NQ][KSTEPS];
+  float qs[PASSES]; // sum of q' over the column's (group, head), score units
+#pragma unroll
+  for (int p = 0; p < PASSES; ++p) {
+    const int cg = (col_id(p) % COLS) / G;
+    float sum = 0.f;
+#pragma unroll
+    for (int j = 0; j < NCH; ++j)
+#pragma unroll
+      for (int m = 0; m < SPC; ++m) {
+        const int ks = j * SPC + m;
+        const int dgrp = ((j * 4 * CH + r * CH) * 8 / Gm::BITS + 8 * m) / GRP;
+        const bool mine = col_live && dgrp == cg;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+          const float v = mine ? raw[ks][slot_elem<FMT>(i)] * a.scale_log2 : 0.f;
+          const _Float16 hi = (_Float16)v;
+          const _Float16 lo = (_Float16)(v - (float)hi);
+          if constexpr (HL) {
+            qb[p][0][ks][i] = col_lo ? lo : hi;
+          } else {
+            qb[p][0][ks][i] = hi;
+            qb[p][NQ - 1][ks][i] = lo;
+          }
+          sum += v;
+        }
+      }
+    sum += __shfl_xor(sum, 16);
+    sum += __shfl_xor(sum, 32);
+    qs[p] = col_lo ? 0.f : sum / UNIT;
+  }
+
+  // ---- per-lane state ----------------------------------------------------------
+  float4_t acc[PASSES][EV];
+#pragma unroll
+  for (int p = 0; p < PASSES; ++p)
+#pragma unroll
+    for (int e = 0; e < EV; ++e) acc[p][e] = (float4_t){0.f, 0.f, 0.f, 0.f};
+  float zacc[PASSES];
+#pragma unroll
+  for (int p = 0; p < PASSES; ++p) zacc[p] = 0.f;
+  float m_run = -INFINITY;  // running max, score units; equal across a head's lanes
+  float m_neg = INFINITY;   // -m_run in log2 units
+  float m_true = -INFINITY; // exact max of this lane's scores, score units
+  float l_sum = 0.f;
+
+  // ---- consume one tile --------------------------------------------------------
+  auto compute = [&](Buf &buf, int k, auto mask_tag) __attribute__((always_inline)) {
+    constexpr bool MASK = decltype(mask_tag)::value;
+    const int tbase = (tile_first + wave + nw * k) * TT;
+    // per-pass (scale, zero) of tokens tau(r, i) for this lane's group
+    uint32_t kmeta[QUANT ? PASSES : 1][8], vmeta[QUANT ? PASSES : 1][8];
+    if constexpr (QMETA) {
+#pragma unroll
+      for (int p = 0; p < PASSES; ++p) {
+        const int g = (col_id(p) % COLS) / G; // the same for the 4 lanes of a quad
+#pragma unroll
+        for (int st = 0; st < 2; ++st) {
+          uint32_t ks = buf.kmr[st].w[0], vs = buf.vmr[st].w[0];
+#pragma unroll
+          for (int gg = 1; gg < NG; ++gg) {
+            ks = g == gg ? buf.kmr[st].w[gg] : ks;
+            vs = g == gg ? buf.vmr[st].w[gg] : vs;
+          }
+          kmeta[p][4 * st + 0] = quad_bcast<0>(ks);
+          kmeta[p][4 * st + 1] = quad_bcast<1>(ks);
+          kmeta[p][4 * st + 2] = quad_bcast<2>(ks);
+          kmeta[p][4 * st + 3] = quad_bcast<3>(ks);
+          vmeta[p][4 * st + 0] = quad_bcast<0>(vs);
+          vmeta[p][4 * st + 1] = quad_bcast<1>(vs);
+          vmeta[p][4 * st + 2] = quad_bcast<2>(vs);
+          vmeta[p][4 * st + 3] = quad_bcast<3>(vs);
+        }
+      }
+    } else if constexpr (QUANT) {
+#pragma unroll
+      for (int p = 0; p < PASSES; ++p)
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+          kmeta[p][i] = buf.km[p][i];
+          vmeta[p][i] = buf.vm[p][i];
+        }
+    }
+    // masked tokens (outside [t0, t1)) carry weight 0; their values are
+    // zeroed too, so a non-finite entry outside the chunk cannot leak in
+    bool ok[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      ok[i] = true;
+      if constexpr (MASK) {
+        const int t = tbase + tau(r, i);
+        ok[i] = t >= t0 && t < t1;
+#pragma unroll
+        for (int w = 0; w < VW; ++w) buf.v[i].w[w] = ok[i] ? buf.v[i].w[w] : 0u;
+        if constexpr (QUANT) {
+#pragma unroll
+          for (int p = 0; p < PASSES; ++p) vmeta[p][i] = ok[i] ? vmeta[p][i] : 0u;
+        }
+      }
+    }
+
+    // ---- scores: QK^T over (group, head) columns, per sub-tile ----------------
+    float s[8];
+#pragma unroll
+    for (int st = 0; st < 2; ++st) {
+      float4_t cq[PASSES];
+#pragma unroll
+      for (int p = 0; p < PASSES; ++p) cq[p] = (float4_t){0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int j = 0; j < NCH; ++j) {
+#pragma unroll
+        for (int m = 0; m < SPC; ++m) {
+          uint32_t aw[4];
+          if constexpr (FMT == FMT_F16) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) aw[i] = buf.k[st][j].w[i];
+          } else if constexpr (FMT == FMT_INT8) {
+            const uint32_t w0 = buf.k[st][j].w[2 * m], w1 = buf.k[st][j].w[2 * m + 1];
+            aw[0] = perm(0u, w0, 0x0c010c00u);
+            aw[1] = perm(0u, w0, 0x0c030c02u);
+            aw[2] = perm(0u, w1, 0x0c010c00u);
+            aw[3] = perm(0u, w1, 0x0c030c02u);
+          } else {
+            const uint32_t w = buf.k[st][j].w[m];
+            const uint32_t lo = w & 0x0F0F0F0Fu, hi = (w >> 4) & 0x0F0F0F0Fu;
+            aw[0] = perm(0u, lo, 0x0c010c00u);
+            aw[1] = perm(0u, lo, 0x0c030c02u);
+            aw[2] = perm(0u, hi, 0x0c010c00u);
+            aw[3] = perm(0u, hi, 0x0c030c02u);
+          }
+          const half8_t av = __builtin_bit_cast(half8_t, (u32x4_t){aw[0], aw[1], aw[2], aw[3]});
+          const int ks = j * SPC + m;
+#pragma unroll
+          for (int p = 0; p < PASSES; ++p)
+#pragma unroll
+            for (int h2 = 0; h2 < NQ; ++h2)
+              cq[p] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av, qb[p][h2][ks], cq[p], 0, 0, 0);
+        }
+      }
+#pragma unroll
+      for (int jj = 0; jj < 4; ++jj) {
+        const int i = 4 * st + jj;
+        float w = 0.f;
+#pragma unroll
+        for (int p = 0; p < PASSES; ++p) {
+          if constexpr (QUANT) {
+            const uint32_t mk = kmeta[p][i];
+            w = fmaf(lo_f(mk), cq[p][jj], fmaf(hi_f(mk), qs[p], w));
+          } else {
+            w += cq[p][jj];
+          }
+        }
+        w = sum_head_cols<G>(w); // the (group, hi/lo) columns of this head
+        s[i] = (MASK && !ok[i]) ? -INFINITY : w;
+      }
+    }
+
+    // ---- online softmax ----------------------------------------------------------
+    const float tmax = fmaxf(fmaxf(fmaxf(s[0], s[1]), fmaxf(s[2], s[3])),
+                             fmaxf(fmaxf(s[4], s[5]), fmaxf(s[6], s[7])));
+    m_true = fmaxf(m_true, tmax);
+    if (__any(tmax > m_run + TAU_S)) { // wave-uniform, rare after the first tile
+      float cand = fmaxf(m_run, tmax);
+      for (int mask = G; mask < 64; mask <<= 1) cand = fmaxf(cand, __shfl_xor(cand, mask));
+      const float alpha =
+          cand == -INFINITY ? 1.f : __builtin_amdgcn_exp2f((m_run - cand) * UNIT);
+      l_sum *= alpha;
+#pragma unroll
+      for (int p = 0; p < PASSES; ++p) zacc[p] *= alpha;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        // accumulator row 4r+i belongs to head (4r+i) mod G: take that
+        // column's alpha
+        const float ai = __shfl(alpha, 16 * r + ((4 * r + i) & 15));
+#pragma unroll
+        for (int p = 0; p < PASSES; ++p)
+#pragma unroll
+          for (int e = 0; e < EV; ++e) acc[p][e][i] *= ai;
+      }
+      m_run = cand;
+      m_neg = -cand * UNIT;
+    }
+    float pj[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) pj[i] = __builtin_amdgcn_exp2f(fmaf(s[i], UNIT, m_neg));
+    l_sum += ((pj[0] + pj[1]) + (pj[2] + pj[3])) + ((pj[4] + pj[5]) + (pj[6] + pj[7]));
+
+    // ---- weights: V scale folded in, binary16 hi/lo -------------------------------
+    half8_t pa[PASSES][NQ];
+#pragma unroll
+    for (int p = 0; p < PASSES; ++p) {
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        float w = pj[i];
+        if constexpr (QUANT) {
+          const uint32_t mv = vmeta[p][i];
+          zacc[p] = fmaf(pj[i], hi_f(mv), zacc[p]);
+          w *= lo_f(mv);
+        }
+        w = col_live ? w : 0.f;
+        const _Float16 hi = (_Float16)w;
+        const _Float16 lo = (_Float16)(w - (float)hi);
+        if constexpr (HL) {
+          pa[p][0][i] = col_lo ? lo : hi;
+        } else {
+          pa[p][0][i] = hi;
+          pa[p][NQ - 1][i] = lo;
+        }
+      }
+    }
+
+    // ---- values: B operand = 8 tokens of one dim, PV MFMA ----------------------------
+#pragma unroll
+    for (int e = 0; e < EV; ++e) {
+      uint32_t bw[4];
+#pragma unroll
+      for (int q2 = 0; q2 < 4; ++q2) {
+        const Raw<VB> &ta = buf.v[2 * q2], &tb = buf.v[2 * q2 + 1];
+        if constexpr (FMT == FMT_F16) {
+          bw[q2] = perm(tb.w[e / 2], ta.w[e / 2], (e & 1) ? 0x07060302u : 0x05040100u);
+        } else if constexpr (FMT == FMT_INT8) {
+          bw[q2] = perm(tb.w[e / 4], ta.w[e / 4], sel_pair(e & 3));
+        } else {
+          const int sh = (e & 1) * 4;
+          const uint32_t na = (ta.w[0] >> sh) & 0x0F0F0F0Fu;
+          const uint32_t nb = (tb.w[0] >> sh) & 0x0F0F0F0Fu;
+          bw[q2] = perm(nb, na, sel_pair((e >> 1) & 3));
+        }
+      }
+      const half8_t bv = __builtin_bit_cast(half8_t, (u32x4_t){bw[0], bw[1], bw[2], bw[3]});
+#pragma unroll
+      for (int p = 0; p < PASSES; ++p)
+#pragma unroll
+        for (int h2 = 0; h2 < NQ; ++h2)
+          acc[p][e] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pa[p][h2], bv, acc[p][e], 0, 0, 0);
+    }
+  };
+
+  // ---- main loop: ring of DEPTH tiles ------------------------------------------
+  for (int kb = 0; kb < nk; kb += DEPTH) {
+    static_for<DEPTH>([&](auto Ui) __attribute__((always_inline)) {
+      constexpr int u = decltype(Ui)::value;
+      Buf &cur = ring(Ui);
+      const int k = kb + u;
+      issue(ring(std::integral_constant<int, (u + DEPTH - 1) % DEPTH>{}), k + DEPTH - 1);
+      if (k < nk) {
+        const int tbase = (tile_first + wave + nw * k) * TT;
+        if (tbase >= t0 && tbase + TT <= t1) compute(cur, k, std::false_type{});
+        else compute(cur, k, std::true_type{});
+      }
+    });
   }
 
   // ---- wave result: per head (m_run, l, m_true) and O[head][D] ---------------
@@ -418,24 +640,48 @@ decode_partial(const Args a, const Ext x, const int G, const int final_out) {
   l_sum += __shfl_xor(l_sum, 32);
   m_true = fmaxf(m_true, __shfl_xor(m_true, 16));
   m_true = fmaxf(m_true, __shfl_xor(m_true, 32));
+  float zrow[PASSES][4];
+#pragma unroll
+  for (int p = 0; p < PASSES; ++p) {
+    float z = zacc[p];
+    z += __shfl_xor(z, 16);
+    z += __shfl_xor(z, 32);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) zrow[p][i] = __shfl(z, 16 * r + ((4 * r + i) & 15));
+  }
+  if constexpr (HL) {
+    // rows 8-15 (lane-rows 2, 3) hold the lo halves of rows 0-7
+#pragma unroll
+    for (int e = 0; e < EV; ++e)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) acc[0][e][i] += __shfl_xor(acc[0][e][i], 32);
+  }
 
   extern __shared__ float smem[];
   // layout: sO[nw][G][D], then sM[nw][G][3]
   float *sO = smem;
   float *sM = smem + nw * G * D;
   if (r == 0 && c < G) {
-    sM[(wave * G + c) * 3 + 0] = m_run;
+    sM[(wave * G + c) * 3 + 0] = m_run * UNIT;
     sM[(wave * G + c) * 3 + 1] = l_sum;
-    sM[(wave * G + c) * 3 + 2] = m_true;
+    sM[(wave * G + c) * 3 + 2] = m_true * UNIT;
   }
+  const int gdim = (c * EV) / GRP; // group of this lane's V dims
 #pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    const int hrow = 4 * r + j;
-    if (hrow < G) {
+  for (int p = 0; p < PASSES; ++p)
 #pragma unroll
-      for (int e = 0; e < EV; ++e) sO[(wave * G + hrow) * D + c * EV + e] = acc[e][j];
+    for (int i = 0; i < 4; ++i) {
+      const int row = p * 16 + 4 * r + i; // (group, head) pair of accumulator row
+      const bool canon = HL ? row < COLS : (PASSES > 1 || row < COLS);
+      if (canon && (row % COLS) / G == gdim) {
+        const int hh = row % G;
+#pragma unroll
+        for (int e = 0; e < EV; ++e) {
+          const float o = QUANT ? fmaf(acc[p][e][i], CODE_SCALE, zrow[p][i]) : acc[p][e][i];
+          sO[(wave * G + hh) * D + c * EV + e] = o;
+        }
+      }
     }
-  }
   __syncthreads();
 
   const int nthreads = nw * 64;
@@ -448,7 +694,7 @@ decode_partial(const Args a, const Ext x, const int G, const int final_out) {
       for (int w2 = 0; w2 < nw; ++w2) {
         const float mr = sM[(w2 * G + hh) * 3 + 0];
         if (mr == -INFINITY) continue;
-        const float wgt = exp2f(mr - M);
+        const float wgt = __builtin_amdgcn_exp2f(mr - M);
         L = fmaf(sM[(w2 * G + hh) * 3 + 1], wgt, L);
         O = fmaf(sO[(w2 * G + hh) * D + col], wgt, O);
       }
@@ -467,57 +713,128 @@ decode_partial(const Args a, const Ext x, const int G, const int final_out) {
       }
     }
   }
-}
 
-// Log-sum-exp recombination of the split partials, one wavefront per head
-// (runtime/kvf_kernels.cuh:288-306 computes the same with D threads).
-template <int D>
-__global__ void __launch_bounds__(64) decode_merge(const Args a, const Ext x) {
-  const int hq = blockIdx.x;
-  const int b = blockIdx.y;
-  const int lane = threadIdx.x;
-  const long long head = (long long)b * a.H + hq;
-  const int S = a.splits;
-  const float *ml = a.part_ml + head * S * 2;
-  float M = -INFINITY;
-  for (int s = lane; s < S; s += 64) M = fmaxf(M, ml[2 * s]);
-#pragma unroll
-  for (int mask = 1; mask < 64; mask <<= 1) M = fmaxf(M, __shfl_xor(M, mask));
-  constexpr int PER = D / 64;
-  float O[PER];
-#pragma unroll
-  for (int i = 0; i < PER; ++i) O[i] = 0.f;
-  float L = 0.f;
-  if (M != -INFINITY) {
-    for (int s = 0; s < S; ++s) {
-      const float ms = ml[2 * s];
-      if (ms == -INFINITY) continue;
-      const float w = exp2f(ms - M);
-      L = fmaf(ml[2 * s + 1], w, L);
-      const float *po = a.part_o + (head * S + s) * D;
-#pragma unroll
-      for (int i = 0; i < PER; ++i) O[i] = fmaf(po[lane + 64 * i], w, O[i]);
+  // ---- fused merge: the last workgroup of a head group combines the splits ----
+  if (!final_out && x.counters) {
+    __shared__ unsigned s_last;
+    unsigned *cnt = x.counters + (long long)b * gridDim.y + hb;
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent"); // this thread's partials
+    __syncthreads();
+    if (threadIdx.x == 0)
+      s_last = __hip_atomic_fetch_add(cnt, 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT) ==
+               (unsigned)(a.splits - 1);
+    __syncthreads();
+    if (s_last) {
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent"); // everyone else's partials
+      const int h_first = G > 1 ? hkv * G : hb;
+      for (int hh = 0; hh < G; ++hh)
+        merge_head<D, WPB * 64>(a, x, (long long)b * a.H + h_first + hh, smem);
+      if (threadIdx.x == 0)
+        __hip_atomic_store(cnt, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
   }
-#pragma unroll
-  for (int i = 0; i < PER; ++i) {
-    const float res = L > 0.f ? O[i] / L : 0.f;
-    if (x.out16) x.out16[head * D + lane + 64 * i] = (_Float16)res;
-    else a.out[head * D + lane + 64 * i] = res;
-  }
 }
 
-template <int FMT, int D, int GQ, int U, int ORD, bool PAGED>
-hipError_t launch_group(const Args &a, const Ext &x, int G, bool partial_only,
-                        hipStream_t st) {
+// Log-sum-exp recombination of the split partials of one head by one
+// workgroup of NT lanes (runtime/kvf_kernels.cuh:288-306 computes the same
+// with one thread per dim walking the splits; empty splits, m = -inf, are
+// skipped there and here). Lane (slice, d) with slice = tid / D sums splits
+// slice, slice + NT/D, ...: all of its partial-output loads are issued at
+// once, while wave 0 loads the split maxima and sums, finds the head's max
+// and writes the split weights to LDS, so a head costs one memory round
+// trip. `lds` holds S + NT floats.
+constexpr int MERGE_CHUNK = 16; // splits per lane per round trip
+
+template <int D, int NT>
+__device__ void merge_head(const Args &a, const Ext &x, long long head, float *lds) {
+  constexpr int SL = NT / D;
+  static_assert(SL >= 1 && NT % D == 0, "merge geometry");
+  const int S = a.splits;
+  const int tid = threadIdx.x, d = tid % D, sl = tid / D;
+  const float *ml = a.part_ml + head * S * 2;
+  const float *po = a.part_o + head * S * D + d;
+  float *sw = lds;          // [S] split weights
+  float *red = lds + S;     // [NT] slice sums, then the head's L
+  float O = 0.f;
+  for (int s0 = 0; s0 < S; s0 += SL * MERGE_CHUNK) {
+    float o[MERGE_CHUNK];
+#pragma unroll
+    for (int i = 0; i < MERGE_CHUNK; ++i) {
+      const int s = s0 + sl + i * SL;
+      o[i] = s < S ? po[(long long)s * D] : 0.f;
+    }
+    if (s0 == 0 && tid < 64) {
+      float M = -INFINITY;
+      for (int s = tid; s < S; s += 64) M = fmaxf(M, ml[2 * s]);
+#pragma unroll
+      for (int m = 1; m < 64; m <<= 1) M = fmaxf(M, __shfl_xor(M, m));
+      float L = 0.f;
+      for (int s = tid; s < S; s += 64) {
+        const float ms = ml[2 * s];
+        const float w = ms == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(ms - M);
+        sw[s] = w;
+        L = fmaf(ml[2 * s + 1], w, L);
+      }
+#pragma unroll
+      for (int m = 1; m < 64; m <<= 1) L += __shfl_xor(L, m);
+      if (tid == 0) red[NT - 1] = L;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < MERGE_CHUNK; ++i) {
+      const int s = s0 + sl + i * SL;
+      if (s < S) O = fmaf(o[i], sw[s], O);
+    }
+  }
+  const float L = red[NT - 1];
+  __syncthreads();
+  red[tid] = O;
+  __syncthreads();
+  if (tid < D) {
+    float o = 0.f;
+#pragma unroll
+    for (int i = 0; i < SL; ++i) o += red[i * D + tid];
+    const float res = L > 0.f ? o / L : 0.f;
+    if (x.out16) x.out16[head * D + tid] = (_Float16)res;
+    else a.out[head * D + tid] = res;
+  }
+  __syncthreads(); // lds is reused by the next head
+}
+
+constexpr int MERGE_THREADS = 512;
+
+// Stand-alone merge: one workgroup per (query head, sequence).
+template <int D>
+__global__ void __launch_bounds__(MERGE_THREADS) decode_merge(const Args a, const Ext x) {
+  extern __shared__ float lds[];
+  merge_head<D, MERGE_THREADS>(a, x, (long long)blockIdx.y * a.H + blockIdx.x, lds);
+}
+
+template <int D>
+inline hipError_t launch_merge_kernel(const Args &a, const Ext &x, hipStream_t st) {
+  hipLaunchKernelGGL((decode_merge<D>), dim3(a.H, a.B), dim3(MERGE_THREADS),
+                     (size_t)(a.splits + MERGE_THREADS) * sizeof(float), st, a, x);
+  return hipGetLastError();
+}
+
+template <int FMT, int D, int GQ, int G, int U, int ORD, bool PAGED>
+hipError_t launch_group(const Args &a, const Ext &x, const Launch &l, hipStream_t st) {
   const dim3 grid(a.splits, G > 1 ? a.Hkv : a.H, a.B);
   const dim3 block(a.warps * 64);
-  const int final_out = (a.splits == 1 && !partial_only) ? 1 : 0;
-  const size_t lds = (size_t)a.warps * G * (D + 3) * sizeof(float);
-  hipLaunchKernelGGL((decode_partial<FMT, D, GQ, U, ORD, PAGED>), grid, block, lds, st,
-                     a, x, G, final_out);
-  if (!final_out && !partial_only)
-    hipLaunchKernelGGL((decode_merge<D>), dim3(a.H, a.B), dim3(64), 0, st, a, x);
+  const int final_out = (a.splits == 1 && !l.partial_only) ? 1 : 0;
+  const bool fused = x.counters && !final_out && !l.partial_only;
+  Ext xk = x;
+  if (!fused) xk.counters = nullptr;
+  size_t lds = (size_t)a.warps * G * (D + 3) * sizeof(float);
+  if (fused) lds = std::max(lds, (size_t)(a.splits + a.warps * 64) * sizeof(float));
+  auto kernel = a.warps == 4 ? &decode_partial<FMT, D, GQ, G, U, ORD, PAGED, 4>
+                             : &decode_partial<FMT, D, GQ, G, U, ORD, PAGED, 8>;
+  if (l.ev_start || l.ev_stop)
+    hipExtLaunchKernelGGL(kernel, grid, block, (uint32_t)lds, st, l.ev_start, l.ev_stop, 0, a, xk,
+                          final_out);
+  else
+    hipLaunchKernelGGL(kernel, grid, block, lds, st, a, xk, final_out);
+  if (!final_out && !l.partial_only && !fused) return launch_merge_kernel<D>(a, x, st);
   return hipGetLastError();
 }
 
@@ -525,6 +842,7 @@ hipError_t launch_group(const Args &a, const Ext &x, int G, bool partial_only,
 inline bool args_ok(const Args &a, int fmt, int D, int G, bool paged) {
   if (a.warps != 4 && a.warps != 8) return false;
   if (a.B < 1 || a.H < 1 || a.Hkv < 1 || a.n < 0 || a.splits < 1) return false;
+  if (a.B > 65535 || a.H > 65535 || a.splits > 65535) return false;
   if (a.H % a.Hkv != 0) return false;
   if (G > 1 && a.H / a.Hkv != G) return false;
   if (!a.q || !a.k || !a.v || !a.out) return false;
@@ -534,23 +852,24 @@ inline bool args_ok(const Args &a, int fmt, int D, int G, bool paged) {
     const int gq = 1 << a.group_shift;
     if (a.group_shift < 5 || a.group_shift > 7 || gq > D) return false;
   }
+  if ((size_t)(a.splits + 512) * sizeof(float) > 60 * 1024) return false; // merge weights in LDS
   if (paged && (a.block_shift < 4 || a.block_shift > 12 || !a.block_table || a.max_blocks < 1))
     return false;
   return true;
 }
 
 template <int FMT, int D, int G, int U, int ORD, bool PAGED>
-hipError_t launch_ext(const Args &a, const Ext &x, bool partial_only, hipStream_t st) {
+hipError_t launch_ext(const Args &a, const Ext &x, const Launch &l, hipStream_t st) {
   if (!args_ok(a, FMT, D, G, PAGED)) return hipErrorInvalidValue;
   if (a.n == 0) return hipErrorInvalidValue;
   if constexpr (FMT == FMT_F16) {
-    return launch_group<FMT, D, 0, U, ORD, PAGED>(a, x, G, partial_only, st);
+    return launch_group<FMT, D, 0, G, U, ORD, PAGED>(a, x, l, st);
   } else {
     switch (a.group_shift) {
-    case 5: return launch_group<FMT, D, 32, U, ORD, PAGED>(a, x, G, partial_only, st);
-    case 6: return launch_group<FMT, D, 64, U, ORD, PAGED>(a, x, G, partial_only, st);
+    case 5: return launch_group<FMT, D, 32, G, U, ORD, PAGED>(a, x, l, st);
+    case 6: return launch_group<FMT, D, 64, G, U, ORD, PAGED>(a, x, l, st);
     default:
-      if constexpr (D >= 128) return launch_group<FMT, D, 128, U, ORD, PAGED>(a, x, G, partial_only, st);
+      if constexpr (D >= 128) return launch_group<FMT, D, 128, G, U, ORD, PAGED>(a, x, l, st);
       return hipErrorInvalidValue;
     }
   }
@@ -561,7 +880,7 @@ hipError_t launch_ext(const Args &a, const Ext &x, bool partial_only, hipStream_
 // The registry-facing template (runtime/kvf_kernels.cuh:309-320 signature).
 template <int FMT, int D, int G, int U, int ORD, bool PAGED>
 hipError_t launch(const Args &a, hipStream_t st) {
-  return gfx950::launch_ext<FMT, D, G, U, ORD, PAGED>(a, gfx950::Ext{}, false, st);
+  return gfx950::launch_ext<FMT, D, G, U, ORD, PAGED>(a, gfx950::Ext{}, gfx950::Launch{}, st);
 }
 
 } // namespace kvf

@@ -23,79 +23,23 @@ namespace kvf {
 namespace gfx950 {
 namespace {
 
-struct Variant {
-  int fmt = -1, ord = -1, paged = -1, g = 0, u = 0, d = 0;
-};
-
-// "{fmt}_{hm|tm}_{c|p}_g{G}_u{U}_d{D}"
-bool parse_variant(const char *id, Variant &v) {
-  if (!id) return false;
-  char fmt[8] = {0}, ord[4] = {0}, res[4] = {0};
-  int g = 0, u = 0, d = 0, used = 0;
-  if (std::sscanf(id, "%7[a-z0-9]_%2[a-z]_%1[a-z]_g%d_u%d_d%d%n", fmt, ord, res, &g, &u, &d,
-                  &used) != 6 || id[used] != '\0')
-    return false;
-  const std::string f(fmt), o(ord), r(res);
-  v.fmt = f == "f16" ? FMT_F16 : f == "int8" ? FMT_INT8 : f == "int4" ? FMT_INT4 : -1;
-  v.ord = o == "hm" ? ORD_HEAD : o == "tm" ? ORD_TOKEN : -1;
-  v.paged = r == "c" ? 0 : r == "p" ? 1 : -1;
-  v.g = g; v.u = u; v.d = d;
-  return v.fmt >= 0 && v.ord >= 0 && v.paged >= 0 && (g == 1 || g == 2 || g == 4 || g == 8) &&
-         (u == 2 || u == 4) && (d == 64 || d == 128);
-}
-
-struct Call {
-  const Args &a;
-  const Ext &x;
-  bool partial;
-  hipStream_t st;
-};
-
-template <int FMT, int D, int G, int U, int ORD, bool PAGED>
-hipError_t go(const Call &c) {
-  return launch_ext<FMT, D, G, U, ORD, PAGED>(c.a, c.x, c.partial, c.st);
-}
-
-template <int FMT, int D, int G, int U>
-hipError_t by_layout(const Variant &v, const Call &c) {
-  if (v.ord == ORD_HEAD)
-    return v.paged ? go<FMT, D, G, U, ORD_HEAD, true>(c) : go<FMT, D, G, U, ORD_HEAD, false>(c);
-  return v.paged ? go<FMT, D, G, U, ORD_TOKEN, true>(c) : go<FMT, D, G, U, ORD_TOKEN, false>(c);
-}
-
-template <int FMT, int D, int G>
-hipError_t by_unroll(const Variant &v, const Call &c) {
-  return v.u == 2 ? by_layout<FMT, D, G, 2>(v, c) : by_layout<FMT, D, G, 4>(v, c);
-}
-
-template <int FMT, int D>
-hipError_t by_pack(const Variant &v, const Call &c) {
-  switch (v.g) {
-  case 1: return by_unroll<FMT, D, 1>(v, c);
-  case 2: return by_unroll<FMT, D, 2>(v, c);
-  case 4: return by_unroll<FMT, D, 4>(v, c);
-  default: return by_unroll<FMT, D, 8>(v, c);
-  }
-}
-
-template <int FMT>
-hipError_t by_dim(const Variant &v, const Call &c) {
-  return v.d == 128 ? by_pack<FMT, 128>(v, c) : by_pack<FMT, 64>(v, c);
-}
-
-hipError_t dispatch(const Variant &v, const Call &c) {
-  switch (v.fmt) {
-  case FMT_F16: return by_dim<FMT_F16>(v, c);
-  case FMT_INT8: return by_dim<FMT_INT8>(v, c);
-  default: return by_dim<FMT_INT4>(v, c);
-  }
-}
-
 Registry &registry() {
   static Registry reg;
   static std::once_flag once;
   std::call_once(once, [] { kvf_register_all(reg); });
   return reg;
+}
+
+LaunchXFn extended(const char *id) { return id ? registry().findx(id) : nullptr; }
+
+Ext ext_of(const kvf_varlen_args_t *va) {
+  Ext x;
+  if (va) {
+    x.seq_lens = va->seq_lens;
+    x.q16 = static_cast<const _Float16 *>(va->q16);
+    x.out16 = static_cast<_Float16 *>(va->out16);
+  }
+  return x;
 }
 
 std::vector<std::string> &variant_ids() {
@@ -203,37 +147,54 @@ extern "C" hipError_t kvf_launch_variant(const char *id, const kvf_args_t *a, hi
 
 extern "C" hipError_t kvf_launch_varlen_variant(const char *id, const kvf_args_t *a,
                                                 const kvf_varlen_args_t *va, hipStream_t st) {
-  Variant v;
-  if (!a || !parse_variant(id, v)) return a ? hipErrorNotFound : hipErrorInvalidValue;
-  if (!registry().find(id)) return hipErrorNotFound;
-  Ext x;
-  if (va) {
-    x.seq_lens = va->seq_lens;
-    x.q16 = static_cast<const _Float16 *>(va->q16);
-    x.out16 = static_cast<_Float16 *>(va->out16);
-  }
-  return dispatch(v, Call{*a, x, false, st});
+  if (!a) return hipErrorInvalidValue;
+  const LaunchXFn fx = extended(id);
+  if (!fx) return hipErrorNotFound;
+  return fx(*a, ext_of(va), Launch{}, st);
+}
+
+extern "C" hipError_t kvf_launch_fused_variant(const char *id, const kvf_args_t *a,
+                                               const kvf_varlen_args_t *va, unsigned *counters,
+                                               hipStream_t st) {
+  if (!a || !counters) return hipErrorInvalidValue;
+  const LaunchXFn fx = extended(id);
+  if (!fx) return hipErrorNotFound;
+  Ext x = ext_of(va);
+  x.counters = counters;
+  return fx(*a, x, Launch{}, st);
 }
 
 extern "C" hipError_t kvf_launch_partial_variant(const char *id, const kvf_args_t *a,
                                                  hipStream_t st) {
-  Variant v;
-  if (!a || !parse_variant(id, v)) return a ? hipErrorNotFound : hipErrorInvalidValue;
-  if (!registry().find(id)) return hipErrorNotFound;
+  if (!a) return hipErrorInvalidValue;
+  const LaunchXFn fx = extended(id);
+  if (!fx) return hipErrorNotFound;
   if (!a->part_o || !a->part_ml) return hipErrorInvalidValue;
-  return dispatch(v, Call{*a, Ext{}, true, st});
+  Launch l;
+  l.partial_only = true;
+  return fx(*a, Ext{}, l, st);
+}
+
+extern "C" hipError_t kvf_launch_partial_variant_timed(const char *id, const kvf_args_t *a,
+                                                       hipStream_t st, hipEvent_t start,
+                                                       hipEvent_t stop) {
+  if (!a) return hipErrorInvalidValue;
+  const LaunchXFn fx = extended(id);
+  if (!fx) return hipErrorNotFound;
+  if (!a->part_o || !a->part_ml || !start || !stop) return hipErrorInvalidValue;
+  Launch l;
+  l.partial_only = true;
+  l.ev_start = start;
+  l.ev_stop = stop;
+  return fx(*a, Ext{}, l, st);
 }
 
 extern "C" hipError_t kvf_launch_merge(int d, const kvf_args_t *a, hipStream_t st) {
   if (!a || a->splits < 1 || a->B < 1 || a->H < 1 || !a->part_o || !a->part_ml || !a->out)
     return hipErrorInvalidValue;
-  if (d == 128)
-    hipLaunchKernelGGL((decode_merge<128>), dim3(a->H, a->B), dim3(64), 0, st, *a, Ext{});
-  else if (d == 64)
-    hipLaunchKernelGGL((decode_merge<64>), dim3(a->H, a->B), dim3(64), 0, st, *a, Ext{});
-  else
-    return hipErrorInvalidValue;
-  return hipGetLastError();
+  if (d == 128) return launch_merge_kernel<128>(*a, Ext{}, st);
+  if (d == 64) return launch_merge_kernel<64>(*a, Ext{}, st);
+  return hipErrorInvalidValue;
 }
 
 extern "C" int kvf_variant_count(void) { return (int)variant_ids().size(); }

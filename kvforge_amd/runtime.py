@@ -67,8 +67,13 @@ def hip_lib():
     L.kvf_launch_varlen_variant.restype = I
     L.kvf_launch_varlen_variant.argtypes = [ctypes.c_char_p, ctypes.POINTER(Args),
                                             ctypes.POINTER(VarlenArgs), P]
+    L.kvf_launch_fused_variant.restype = I
+    L.kvf_launch_fused_variant.argtypes = [ctypes.c_char_p, ctypes.POINTER(Args),
+                                           ctypes.POINTER(VarlenArgs), P, P]
     L.kvf_launch_partial_variant.restype = I
     L.kvf_launch_partial_variant.argtypes = [ctypes.c_char_p, ctypes.POINTER(Args), P]
+    L.kvf_launch_partial_variant_timed.restype = I
+    L.kvf_launch_partial_variant_timed.argtypes = [ctypes.c_char_p, ctypes.POINTER(Args), P, P, P]
     L.kvf_launch_merge.restype = I
     L.kvf_launch_merge.argtypes = [I, ctypes.POINTER(Args), P]
     L.kvf_variant_count.restype = I
@@ -162,6 +167,22 @@ def launch_partial(vid, args, stream=None):
     err = hip_lib().kvf_launch_partial_variant(vid.encode(), ctypes.byref(args),
                                                stream_handle(stream))
     check(err, f"kvf_launch_partial_variant({vid})")
+
+
+def launch_fused(vid, args, counters, varlen=None, stream=None):
+    """One-launch decode step (split kernel + in-kernel merge); `counters` is a
+    zeroed int32 device tensor of B * grid_y entries, left zero afterwards."""
+    va = None
+    if varlen is not None:
+        seq_lens, q16, out16 = varlen
+        va = VarlenArgs()
+        va.seq_lens = seq_lens.data_ptr() if seq_lens is not None else None
+        va.q16 = q16.data_ptr() if q16 is not None else None
+        va.out16 = out16.data_ptr() if out16 is not None else None
+        va = ctypes.byref(va)
+    err = hip_lib().kvf_launch_fused_variant(vid.encode(), ctypes.byref(args), va,
+                                             _ptr(counters), stream_handle(stream))
+    check(err, f"kvf_launch_fused_variant({vid})")
 
 
 def launch_merge(d, args, stream=None):

@@ -223,3 +223,25 @@ def test_bad_arguments_are_rejected():
     assert R.hip_lib().kvf_launch_variant(b"int8_hm_c_g4_u2_d96", a, None) == R.HIP_ERROR_NOT_FOUND
     a.group_shift = 4
     assert R.hip_lib().kvf_launch_variant(b"int8_hm_c_g4_u2_d128", a, None) == R.HIP_ERROR_INVALID_VALUE
+
+
+@pytest.mark.parametrize("fmt,group,order,bt,G", [
+    (R.FMT_INT8, 64, R.ORD_HEAD, 0, 4), (R.FMT_F16, 0, R.ORD_TOKEN, 16, 4),
+    (R.FMT_INT4, 32, R.ORD_HEAD, 32, 8), (R.FMT_INT8, 128, R.ORD_TOKEN, 0, 1)])
+def test_fused_merge_matches_two_launch(fmt, group, order, bt, G):
+    # one-launch step (last workgroup merges) against the two-launch step
+    H = 32 if G in (1, 4) else 16
+    Hkv = H // 4 if G == 1 else H // G
+    b = build(Case(2, H, Hkv, 128, 1500, fmt, group, order, bt, seed=11))
+    counters = torch.zeros(2 * (Hkv if G > 1 else H), dtype=torch.int32, device="cuda:0")
+    for splits, warps, unroll in ((8, 4, 2), (13, 8, 4), (64, 4, 4)):
+        two = run(b, splits, pack=G > 1, unroll=unroll, warps=warps)
+        b.out.fill_(float("nan"))
+        a = args(b, splits, warps)
+        for _ in range(2):  # the second call reuses the counters left at zero
+            R.launch_fused(vid(b, G > 1, unroll), a, counters)
+        torch.cuda.synchronize()
+        fused = b.out.cpu().numpy()
+        assert int(counters.abs().sum()) == 0
+        check(b, fused, f"fused S={splits} w{warps} u{unroll}")
+        assert np.max(np.abs(fused - two)) <= 1e-5 * max(1.0, float(np.max(np.abs(two))))
