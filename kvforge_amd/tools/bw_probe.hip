@@ -114,6 +114,14 @@ __global__ void fma_chain(float *out, int iters) {
 
 __global__ void empty_kernel() {}
 
+// Plain copy of n_vec 16-byte vectors: the calibration kernel for the
+// FETCH_SIZE / WRITE_SIZE counters (known bytes read and written).
+__global__ void copy_kernel(const u32x4 *__restrict__ src, u32x4 *__restrict__ dst, size_t n_vec) {
+  const size_t stride = (size_t)gridDim.x * blockDim.x;
+  for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n_vec; i += stride)
+    __builtin_nontemporal_store(__builtin_nontemporal_load(src + i), dst + i);
+}
+
 // One 16-byte load and one store per lane: a single memory round trip.
 __global__ void one_trip(const u32x4 *__restrict__ p, unsigned *out) {
   const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
@@ -316,6 +324,17 @@ int main(int argc, char **argv) {
   }
   std::fflush(stdout);
 
+  // ---- copy: 512 MiB read + 512 MiB written (counter calibration) ---------------------
+  double bw_copy = 0;
+  {
+    const size_t cbytes = 512ull << 20;
+    const double us = best_us(
+        [&] { hipLaunchKernelGGL(copy_kernel, dim3(cus * 4), dim3(256), 0, 0, big, big + (cbytes / 16), cbytes / 16); },
+        1, 3);
+    bw_copy = 2.0 * cbytes / (us * 1e3);
+    std::printf("  copy     = %.0f GB/s (512 MiB read + 512 MiB written per launch)\n", bw_copy);
+  }
+
   // ---- L2 and MALL bandwidth: working sets that fit each level ---------------------------
   const size_t l2_ws = (size_t)std::max<long long>(1 << 20, l2 / 2);
   const int l2_passes = 200;
@@ -419,6 +438,7 @@ int main(int argc, char **argv) {
   std::fprintf(f, "mall_bytes = %lld\n", mall);
   std::fprintf(f, "bw_mall_gbs = %.0f\n", bw_mall);
   std::fprintf(f, "lat_mall_ns = %.0f\n", lat_mall_ns);
+  std::fprintf(f, "bw_copy_gbs = %.0f\n", bw_copy);
   std::fprintf(f, "kernel_floor_us = %.2f\n", floor_us);
   std::fprintf(f, "round_trip_us = %.2f\n", trip_us);
   if (path) {
