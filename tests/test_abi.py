@@ -1,0 +1,80 @@
+"""The C-ABI library loads without a GPU and exports every function that
+include/*.h declares with C linkage; Args keeps the reference's layout
+(runtime/kvf_kernels.cuh:29-46: 9 pointers, 9 ints, 1 float). No kernel is
+launched here."""
+import ctypes
+import os
+import re
+
+import pytest
+
+from kvforge_amd import runtime as R
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+INCLUDE = os.path.join(ROOT, "include")
+
+
+def _c_functions(path):
+    """Names of the functions declared inside the header's extern "C" block."""
+    text = open(path).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    text = re.sub(r"//[^\n]*", "", text)
+    names = []
+    for block in re.findall(r'extern "C" \{(.*?)\n\}', text, flags=re.S):
+        for m in re.finditer(r"\b([A-Za-z_][A-Za-z0-9_]*)\s*\(", block):
+            name = m.group(1)
+            if name.startswith("kvf_"):
+                names.append(name)
+    return names
+
+
+def test_header_declares_entry_points():
+    names = _c_functions(os.path.join(INCLUDE, "kvf_abi.h"))
+    for must in ("kvf_launch_variant", "kvf_launch_merge", "kvf_quantize_place",
+                 "kvf_variant_count", "kvf_variant_id"):
+        assert must in names
+    assert len(names) == len(set(names))
+
+
+@pytest.mark.skipif(not os.path.exists(R.HIP_LIB), reason="libkvf_hip.so not built")
+def test_library_exports_every_declared_symbol():
+    lib = ctypes.CDLL(R.HIP_LIB)
+    missing = []
+    for h in sorted(os.listdir(INCLUDE)):
+        if h.endswith(".h"):
+            for name in _c_functions(os.path.join(INCLUDE, h)):
+                if not hasattr(lib, name):
+                    missing.append(f"{h}:{name}")
+    assert not missing, missing
+
+
+@pytest.mark.skipif(not os.path.exists(R.HIP_LIB), reason="libkvf_hip.so not built")
+def test_registry_is_populated_without_a_gpu():
+    # the registry is filled by static code; listing it touches no device
+    lib = R.hip_lib()
+    n = lib.kvf_variant_count()
+    ids = {lib.kvf_variant_id(i).decode() for i in range(n)}
+    # the reference's gen/ tables hold 144 ids (12 buckets x G{1,4,8} x U{2,4}
+    # x D{64,128}); G=2 is added because plan enumeration packs g=2 groups
+    # (src/plan.cpp:37-86) and would otherwise name a variant nobody compiled
+    assert n == 192 and len(ids) == 192
+    for fmt in ("f16", "int8", "int4"):
+        for o in ("hm", "tm"):
+            for r in ("c", "p"):
+                for g in (1, 2, 4, 8):
+                    for u in (2, 4):
+                        for d in (64, 128):
+                            assert f"{fmt}_{o}_{r}_g{g}_u{u}_d{d}" in ids
+    assert lib.kvf_version().decode()
+
+
+def test_args_layout_matches_reference():
+    a = R.Args
+    names = [f[0] for f in a._fields_]
+    assert names == ["q", "k", "v", "k_meta", "v_meta", "block_table", "out", "part_o",
+                     "part_ml", "B", "H", "Hkv", "n", "splits", "warps", "group_shift",
+                     "block_shift", "max_blocks", "scale_log2"]
+    p = ctypes.sizeof(ctypes.c_void_p)
+    assert a.B.offset == 9 * p
+    assert a.scale_log2.offset == 9 * p + 9 * 4
+    assert ctypes.sizeof(a) == 9 * p + 9 * 4 + 4
