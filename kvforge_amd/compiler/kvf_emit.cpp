@@ -1,0 +1,356 @@
+// kvf_emit.cpp - plan outputs and dispatch sources of the kvf compiler.
+#include "kvf_emit.h"
+
+#include <algorithm>
+#include <fstream>
+#include <iomanip>
+#include <set>
+#include <sstream>
+#include <stdexcept>
+
+namespace kvfc {
+
+namespace {
+
+void save(const std::filesystem::path &p, const std::string &text) {
+  std::ofstream o(p, std::ios::binary);
+  if (!o) throw std::runtime_error("cannot write " + p.string());
+  o << text;
+}
+
+std::string fx(double v, int prec) {
+  std::ostringstream o;
+  o << std::fixed << std::setprecision(prec) << v;
+  return o.str();
+}
+
+std::string col(const std::string &s, std::size_t w, bool right = false) {
+  if (s.size() >= w) return s;
+  const std::string fill(w - s.size(), ' ');
+  return right ? fill + s : s + fill;
+}
+
+const char *fmtConstant(Format f) {
+  switch (f) {
+  case Format::F16: return "kvf::FMT_F16";
+  case Format::INT8: return "kvf::FMT_INT8";
+  case Format::INT4: return "kvf::FMT_INT4";
+  case Format::Unset: break;
+  }
+  throw std::runtime_error("codegen: format not resolved");
+}
+
+const char *ordConstant(Order o) {
+  switch (o) {
+  case Order::HeadMajor: return "kvf::ORD_HEAD";
+  case Order::TokenMajor: return "kvf::ORD_TOKEN";
+  case Order::Unset: break;
+  }
+  throw std::runtime_error("codegen: order not resolved");
+}
+
+int packOf(const Plan &p, int g) { return p.part.gqa_pack ? g : 1; }
+
+// Template arguments of the launcher a plan needs: <FMT, D, G, U, ORD, PAGED>.
+std::string templateArgs(const Plan &p, int g, int d) {
+  std::ostringstream o;
+  o << "<" << fmtConstant(p.fmt.fmt) << ", " << d << ", " << packOf(p, g) << ", " << p.part.unroll << ", "
+    << ordConstant(p.layout.order) << ", " << (p.layout.paged() ? "true" : "false") << ">";
+  return o.str();
+}
+
+int ilog2(int v) {
+  int s = 0;
+  while ((1 << s) < v) ++s;
+  return s;
+}
+
+const Operation &planned(const Module &m) {
+  const Operation &op = m.attn();
+  if (!op.planned) throw std::runtime_error("emit: module was not planned");
+  return op;
+}
+
+std::string mib(double bytes) { return fx(bytes / (1024.0 * 1024.0), 2) + " MiB"; }
+
+} // namespace
+
+std::string variantId(const Plan &p, int g, int d) {
+  std::ostringstream o;
+  o << formatName(p.fmt.fmt) << "_" << (p.layout.order == Order::HeadMajor ? "hm" : "tm") << "_"
+    << (p.layout.paged() ? "p" : "c") << "_g" << packOf(p, g) << "_u" << p.part.unroll << "_d" << d;
+  return o.str();
+}
+
+// Column layout and number formatting (default stream precision) follow
+// src/emit.cpp:77-97 so that the file is interchangeable with the
+// reference's.
+std::string plansCsv(const Module &m) {
+  const DecodeSpec &s = m.spec;
+  std::ostringstream o;
+  o << "name,H,H_kv,d,n,batch,fmt,group,order,residency,block_tokens,splits,gqa_pack,warps,unroll,"
+       "pred_us,pred_gbs,pred_eta,pred_mem_us,pred_cmp_us,pred_merge_us,pred_page_us,blocks,active_sms,"
+       "rel_err,rejected\n";
+  for (const auto &r : m.ranked) {
+    const Plan &p = r.plan;
+    const Cost &c = r.cost;
+    o << s.name << ',' << s.H << ',' << s.H_kv << ',' << s.d << ',' << s.n << ',' << s.batch << ','
+      << formatName(p.fmt.fmt) << ',' << p.fmt.group << ',' << orderName(p.layout.order) << ','
+      << residencyName(p.layout.residency) << ',' << p.layout.block_tokens << ',' << p.part.splits << ','
+      << (p.part.gqa_pack ? 1 : 0) << ',' << p.part.warps << ',' << p.part.unroll << ',' << c.t_total_us << ','
+      << c.achieved_gbs << ',' << c.eta << ',' << c.t_mem_us << ',' << c.t_cmp_us << ',' << c.t_merge_us << ','
+      << c.t_page_us << ',' << c.blocks << ',' << c.active_sms << ',' << c.rel_err << ','
+      << (c.rejected ? 1 : 0) << "\n";
+  }
+  return o.str();
+}
+
+std::string rooflineText(const Module &m) {
+  const DecodeSpec &s = m.spec;
+  const Machine &mc = m.machine;
+  const double ridge = mc.ridgeFlopPerByte();
+  std::ostringstream o;
+  o << "Roofline: decode attention on " << mc.name << "\n";
+  o << "  ridge point " << fx(ridge, 2) << " FLOP/byte = " << fx(mc.f32_gflops / 1000.0, 2) << " TFLOP/s / "
+    << fx(mc.bw_peak_gbs, 1) << " GB/s\n";
+  o << "  every query head does 4*n*d FLOPs against 2*n*d*b_eff bytes of its KV head, so the\n"
+    << "  intensity 2*g/b_eff is independent of n (b_eff = bytes per stored element, metadata included)\n\n";
+  o << col("format", 12) << col("b_eff bits", 12, true) << col("I(g=1)", 10, true) << col("I(g=4)", 10, true)
+    << col("I(g=8)", 10, true) << "   at g=" << s.g() << "\n";
+  o << std::string(74, '-') << "\n";
+  for (const auto &f : candidateFormats(s.d, true)) {
+    o << col(f.str(), 12) << col(fx(f.effectiveBits(), 2), 12, true);
+    for (int g : {1, 4, 8}) {
+      DecodeSpec t = s;
+      t.H_kv = std::max(1, s.H / g);
+      o << col(fx(idealIntensity(t, f), 2), 10, true);
+    }
+    o << "   " << (idealIntensity(s, f) < ridge ? "memory bound" : "compute bound") << "\n";
+  }
+  o << "\nA quantized element costs its code bits plus 32 bits of (scale, zero) per group:\n"
+    << "int4:128 stores 4 + 32/128 = 4.25 bits per element.\n";
+  return o.str();
+}
+
+std::string reportText(const Module &m, const std::string &ir_before, int top_n) {
+  const Operation &op = planned(m);
+  const Cost &c = op.cost;
+  const DecodeSpec &s = m.spec;
+  const Machine &mc = m.machine;
+  std::ostringstream o;
+  o << "kvf plan: " << s.name << "\n" << std::string(10 + s.name.size(), '=') << "\n\n";
+  o << "Decode attention, one layer, one step: each cached byte is read once and used once,\n"
+    << "so a plan is judged by the bytes it moves and how well it keeps the memory system busy.\n\n";
+  o << "shape    H = " << s.H << ", H_kv = " << s.H_kv << " (g = " << s.g() << "), d = " << s.d << ", n = " << s.n
+    << ", batch = " << s.batch << ", scale = " << op.scale << "\n";
+  o << "machine  " << mc.name;
+  if (!m.machine_file.empty()) o << " [" << m.machine_file << "]";
+  o << "\n         " << mc.sms << (mc.cdna() ? " CUs (64-lane wavefronts)" : " SMs (32-lane warps)")
+    << ", peak " << fx(mc.bw_peak_gbs, 1) << " GB/s, per unit " << fx(mc.bw_sm_gbs, 1) << " GB/s, latency "
+    << fx(mc.lat_ns, 0) << " ns, ridge " << fx(mc.ridgeFlopPerByte(), 2) << " FLOP/byte\n";
+  o << "model    " << (mc.cdna() ? "CDNA (gfx950 tile kernels)" : "warp (reference kernels)")
+    << ", constants " << (m.calib_file.empty() ? "defaults" : m.calib_file) << "\n";
+  o << "search   format " << (m.space.format_free ? "free" : "pinned") << ", layout "
+    << (m.space.layout_free ? "free" : "pinned") << ", splits " << (m.space.splits_free ? "free" : "pinned")
+    << ", gqa_pack " << (m.space.pack_free ? "free" : "pinned") << "; lossy formats "
+    << (m.space.include_quantized ? "included" : "excluded");
+  if (m.space.max_rel_err > 0) o << " (accuracy limit " << m.space.max_rel_err << ")";
+  o << "; " << m.ranked.size() << " candidates\n\n";
+
+  o << "Chosen plan\n";
+  o << "  format:    " << op.plan.fmt.str() << "  (" << fx(op.plan.fmt.effectiveBits(), 2) << " bits/element";
+  if (op.plan.fmt.isQuantized()) o << ", calibrated relative error " << c.rel_err;
+  o << ")\n";
+  o << "  layout:    " << op.plan.layout.str() << "\n";
+  o << "  partition: " << op.plan.part.str() << "  -> " << c.blocks << " workgroups on " << c.active_sms
+    << (mc.cdna() ? " CUs" : " SMs") << "\n";
+  o << "  variant:   " << variantId(op.plan, s.g(), s.d) << "\n\n";
+
+  o << "Predicted cost\n";
+  auto line = [&](const char *k, const std::string &v, const char *unit) {
+    o << "  " << col(k, 20) << col(v, 12, true) << (*unit ? " " : "") << unit << "\n";
+  };
+  line("KV payload", mib(c.kv_bytes), "");
+  line("group metadata", mib(c.meta_bytes), "");
+  line("query + output", mib(c.qo_bytes), "");
+  line("split partials", mib(c.partial_bytes), "");
+  line("total traffic", mib(c.total_bytes), "");
+  line("attention FLOPs", fx(c.attn_flops / 1e6, 2), "M");
+  line("dequant FLOPs", fx(c.dequant_flops / 1e6, 2), "M");
+  line("intensity", fx(c.intensity, 3), "FLOP/byte");
+  line("run efficiency", fx(c.eta, 3), "");
+  line("bytes in flight", fx(c.bif_sm_bytes / 1024.0, 1), mc.cdna() ? "KiB per CU" : "KiB per SM");
+  line("effective bandwidth", fx(c.bw_eff_gbs, 1), "GB/s");
+  line("T_mem", fx(c.t_mem_us, 2), "us");
+  line("T_cmp", fx(c.t_cmp_us, 2), "us");
+  line("T_merge", fx(c.t_merge_us, 2), "us");
+  line("T_page", fx(c.t_page_us, 2), "us");
+  line("T_launch", fx(c.t_launch_us, 2), "us");
+  line("T_total", fx(c.t_total_us, 2), c.memory_bound ? "us (memory bound)" : "us (issue bound)");
+  o << "  " << col("achieved", 20) << col(fx(c.achieved_gbs, 1), 12, true) << " GB/s = "
+    << fx(100.0 * c.frac_of_peak, 1) << "% of peak\n\n";
+
+  o << "Ranking\n";
+  o << col("rank", 6) << col("plan", 58) << col("us", 10, true) << col("GB/s", 9, true) << col("%peak", 8, true)
+    << col("FLOP/B", 8, true) << col("WGs", 8, true) << col("eta", 7, true) << "  bound  gate\n";
+  o << std::string(122, '-') << "\n";
+  const std::size_t limit = top_n > 0 ? std::min<std::size_t>(top_n, m.ranked.size()) : m.ranked.size();
+  for (std::size_t i = 0; i < limit; ++i) {
+    const Ranked &r = m.ranked[i];
+    o << col(std::to_string(i + 1), 6) << col(r.plan.str(), 58) << col(fx(r.cost.t_total_us, 2), 10, true)
+      << col(fx(r.cost.achieved_gbs, 1), 9, true) << col(fx(100.0 * r.cost.frac_of_peak, 1), 8, true)
+      << col(fx(r.cost.intensity, 2), 8, true) << col(std::to_string(r.cost.blocks), 8, true)
+      << col(fx(r.cost.eta, 2), 7, true) << "  " << col(r.cost.memory_bound ? "mem" : "issue", 7)
+      << (r.cost.rejected ? r.cost.note : "ok") << "\n";
+  }
+  if (limit < m.ranked.size()) o << "(" << (m.ranked.size() - limit) << " more in plans.csv)\n";
+  o << "\n" << rooflineText(m) << "\n";
+  o << "Module before planning\n" << ir_before << "\nModule after planning\n" << printModule(m);
+  return o.str();
+}
+
+// The plan's translation unit: the launcher copies the caller's Args, sets
+// the four fields the plan fixes (splits, waves per workgroup, group and page
+// shifts) and calls the one instantiation the plan names. Built with hipcc
+// for gfx950 against kvforge_amd/csrc.
+std::string kernelSource(const Module &m) {
+  const Operation &op = planned(m);
+  const Plan &p = op.plan;
+  const DecodeSpec &s = m.spec;
+  std::ostringstream o;
+  o << "// Generated by kvf for " << (m.machine.cdna() ? "gfx950" : "a 32-lane-warp machine file")
+    << " (HIP). Do not edit.\n";
+  o << "// decode " << s.name << ": H=" << s.H << " H_kv=" << s.H_kv << " d=" << s.d << " n=" << s.n
+    << " batch=" << s.batch << "\n";
+  o << "// plan: " << p.str() << "\n";
+  o << "// predicted: " << op.cost.t_total_us << " us, " << op.cost.achieved_gbs << " GB/s on " << m.machine.name
+    << "\n";
+  o << "#include \"kvf_kernels.hpp\"\n\n";
+  o << "extern \"C\" hipError_t kvf_launch_" << s.name << "(const kvf::Args *in, hipStream_t st) {\n";
+  o << "  kvf::Args a = *in;\n";
+  o << "  a.splits = " << p.part.splits << ";\n";
+  o << "  a.warps = " << p.part.warps << ";\n";
+  if (p.fmt.isQuantized()) o << "  a.group_shift = " << ilog2(p.fmt.group) << ";\n";
+  if (p.layout.paged()) o << "  a.block_shift = " << ilog2(p.layout.block_tokens) << ";\n";
+  o << "  return kvf::launch" << templateArgs(p, s.g(), s.d) << "(a, st);\n";
+  o << "}\n\n";
+  o << "extern \"C\" const char *kvf_plan_" << s.name << "() { return \"" << p.str() << "\"; }\n";
+  return o.str();
+}
+
+// Macro names are the reference's (src/codegen.cpp:95-116), read by drivers
+// written against plan_info.h.
+std::string planHeader(const Module &m) {
+  const Operation &op = planned(m);
+  const Plan &p = op.plan;
+  const DecodeSpec &s = m.spec;
+  std::ostringstream o;
+  o << "// Generated by kvf. Do not edit.\n#pragma once\n";
+  auto def = [&](const char *k, const std::string &v) { o << "#define " << k << " " << v << "\n"; };
+  def("KVF_NAME", s.name);
+  def("KVF_LAUNCH", "kvf_launch_" + s.name);
+  def("KVF_PLAN", "kvf_plan_" + s.name);
+  def("KVF_H", std::to_string(s.H));
+  def("KVF_HKV", std::to_string(s.H_kv));
+  def("KVF_D", std::to_string(s.d));
+  def("KVF_N", std::to_string(s.n));
+  def("KVF_BATCH", std::to_string(s.batch));
+  def("KVF_FMT", fmtConstant(p.fmt.fmt));
+  def("KVF_GROUP", std::to_string(p.fmt.group));
+  def("KVF_ORDER", ordConstant(p.layout.order));
+  def("KVF_PAGED", p.layout.paged() ? "1" : "0");
+  def("KVF_BLOCK", std::to_string(p.layout.block_tokens));
+  def("KVF_SPLITS", std::to_string(p.part.splits));
+  def("KVF_WARPS", std::to_string(p.part.warps));
+  std::ostringstream us;
+  us << op.cost.t_total_us;
+  def("KVF_PRED_US", us.str());
+  return o.str();
+}
+
+Written writePlanOutputs(const Module &m, const std::filesystem::path &dir, const std::string &ir_before,
+                         int top_n) {
+  std::filesystem::create_directories(dir);
+  Written w;
+  w.report = dir / "report.txt";
+  w.plans_csv = dir / "plans.csv";
+  w.ir_txt = dir / "ir.txt";
+  w.kernel = dir / ("decode_" + m.spec.name + ".hip");
+  save(w.report, reportText(m, ir_before, top_n));
+  save(w.plans_csv, plansCsv(m));
+  save(w.ir_txt, "before planning\n" + ir_before + "\nafter planning\n" + printModule(m));
+  save(w.kernel, kernelSource(m));
+  save(dir / "plan_info.h", planHeader(m));
+  return w;
+}
+
+std::vector<std::pair<std::string, std::string>> dispatchSources(const std::vector<int> &dims,
+                                                                 const std::vector<int> &packs,
+                                                                 bool include_quantized) {
+  std::vector<Format> fmts{Format::F16};
+  if (include_quantized) {
+    fmts.push_back(Format::INT8);
+    fmts.push_back(Format::INT4);
+  }
+  std::set<int> pack_set{1};
+  for (int g : packs)
+    if (g == 2 || g == 4 || g == 8) pack_set.insert(g);
+
+  std::vector<std::pair<std::string, std::string>> files;
+  std::vector<std::string> buckets;
+  for (Format f : fmts)
+    for (Order ord : {Order::HeadMajor, Order::TokenMajor})
+      for (bool paged : {false, true}) {
+        const std::string bucket = std::string(formatName(f)) + (ord == Order::HeadMajor ? "_hm" : "_tm") +
+                                   (paged ? "_p" : "_c");
+        buckets.push_back(bucket);
+        auto planOf = [&](int g, int u) {
+          Plan p;
+          p.fmt.fmt = f;
+          p.layout.order = ord;
+          p.layout.residency = paged ? Residency::Paged : Residency::Contiguous;
+          p.part.gqa_pack = g > 1;
+          p.part.unroll = u;
+          return p;
+        };
+        // registration: the reference's launcher plus the extended one
+        std::ostringstream reg;
+        reg << "// Generated by kvf. Do not edit.\n#include \"kvf_ext.hpp\"\n#include \"kvf_registry.h\"\n\n";
+        reg << "void kvf_register_" << bucket << "(kvf::Registry &r) {\n";
+        for (int d : dims)
+          for (int g : pack_set)
+            for (int u : {2, 4}) {
+              const Plan p = planOf(g, u);
+              const std::string t = templateArgs(p, g, d);
+              reg << "  r.add(\"" << variantId(p, g, d) << "\", &kvf::launch" << t << ",\n"
+                  << "        &kvf::gfx950::launch_ext" << t << ");\n";
+            }
+        reg << "}\n";
+        files.emplace_back("kvf_dispatch_" + bucket + ".hip", reg.str());
+        // explicit instantiations, one file per head dimension so they build in parallel
+        for (int d : dims) {
+          std::ostringstream inst;
+          inst << "// Generated by kvf. Do not edit.\n"
+               << "// Explicit instantiations of one dispatch bucket and head dimension; the\n"
+               << "// bucket file registers their addresses.\n#include \"kvf_kernels.hpp\"\n\n";
+          for (int g : pack_set)
+            for (int u : {2, 4}) {
+              const std::string t = templateArgs(planOf(g, u), g, d);
+              inst << "template hipError_t kvf::launch" << t << "(const kvf::Args &, hipStream_t);\n"
+                   << "template hipError_t kvf::gfx950::launch_ext" << t << "(\n"
+                   << "    const kvf::Args &, const kvf::gfx950::Ext &, const kvf::gfx950::Launch &, hipStream_t);\n";
+            }
+          files.emplace_back("kvf_inst_" + bucket + "_d" + std::to_string(d) + ".hip", inst.str());
+        }
+      }
+  std::ostringstream all;
+  all << "// Generated by kvf. Do not edit.\n#include \"kvf_registry.h\"\n\n";
+  for (const auto &b : buckets) all << "void kvf_register_" << b << "(kvf::Registry &r);\n";
+  all << "\nvoid kvf_register_all(kvf::Registry &r) {\n";
+  for (const auto &b : buckets) all << "  kvf_register_" << b << "(r);\n";
+  all << "}\n";
+  files.emplace_back("kvf_dispatch.hip", all.str());
+  return files;
+}
+
+} // namespace kvfc

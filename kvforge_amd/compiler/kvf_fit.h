@@ -1,0 +1,58 @@
+// kvf_fit.h - measured sweeps against the cost model: loading, scoring and
+// fitting the model's constants.
+//
+// Restates the reference's src/fit.cpp:101-325: sweep CSV columns, the
+// per-shape metrics (MAPE, Spearman, Kendall, selection regret, top-1) and
+// the coordinate-grid calibration with its loss (mean |log error| plus the
+// mean regret over the three eligibility classes), so a sweep fitted here
+// yields the constants the reference fits.
+#pragma once
+
+#include "kvf_model.h"
+
+#include <filesystem>
+#include <functional>
+#include <string>
+#include <vector>
+
+namespace kvfc {
+
+struct SweepRow {
+  DecodeSpec spec;
+  Plan plan;
+  double t_us = 0; // median measured time of one decode step
+  double t_p25 = 0, t_p75 = 0;
+  double err_exact = 0; // relative L2 error against exact attention
+  bool verified = true; // output matched the dequantised reference
+};
+
+// Rows with t_us > 0; columns by name, so extra columns are ignored.
+std::vector<SweepRow> loadSweep(const std::filesystem::path &p);
+std::string shapeKey(const DecodeSpec &s); // "H32_Hkv8_d128_n32768_b1"
+
+struct Metrics {
+  int rows = 0, shapes = 0;
+  double mape = 0, spearman = 0, kendall = 0;
+  double regret_mean = 0, regret_max = 0, top1 = 0;
+  std::string per_shape;
+};
+
+struct Eligibility {
+  double max_rel_err = 0;           // 0: every format
+  std::vector<std::string> formats; // empty: every format
+};
+
+using ShapeFilter = std::function<bool(const std::string &)>;
+
+Metrics evaluateSweep(const std::vector<SweepRow> &rows, const Machine &m, const Calib &c, const Eligibility &e,
+                      const ShapeFilter &use);
+Calib calibrate(const std::vector<SweepRow> &rows, const Machine &m, const Calib &start, const ShapeFilter &use);
+
+// Every `every`-th distinct shape in key order is held out of the fit.
+std::vector<std::string> heldOutShapes(const std::vector<SweepRow> &rows, int every);
+
+// The three eligibility classes a user can ask for, scored and printed.
+std::string evaluationReport(const std::vector<SweepRow> &rows, const Machine &m, const Calib &c,
+                             const ShapeFilter &use);
+
+} // namespace kvfc

@@ -1,0 +1,591 @@
+// kvf_front.cpp - scanner, parser, lowering and planner of the kvf compiler.
+#include "kvf_front.h"
+
+#include <cctype>
+#include <cmath>
+#include <filesystem>
+#include <map>
+#include <set>
+#include <sstream>
+#include <stdexcept>
+
+namespace kvfc {
+
+// ======================================================================= scanner
+std::vector<Token> scanSource(const std::string &src) {
+  std::vector<Token> out;
+  std::size_t i = 0;
+  int line = 1, col = 1;
+  auto at = [&](std::size_t k) { return k < src.size() ? src[k] : '\0'; };
+  auto bump = [&]() {
+    if (src[i] == '\n') {
+      ++line;
+      col = 1;
+    } else {
+      ++col;
+    }
+    ++i;
+  };
+  while (true) {
+    // whitespace and comments
+    while (i < src.size()) {
+      const unsigned char c = static_cast<unsigned char>(src[i]);
+      if (std::isspace(c)) {
+        bump();
+      } else if (c == '#' || (c == '/' && at(i + 1) == '/')) {
+        while (i < src.size() && src[i] != '\n') bump();
+      } else {
+        break;
+      }
+    }
+    Token t;
+    t.line = line;
+    t.col = col;
+    if (i >= src.size()) {
+      out.push_back(t);
+      return out;
+    }
+    const unsigned char c = static_cast<unsigned char>(src[i]);
+    if (std::isalpha(c) || c == '_') {
+      t.kind = TokKind::Word;
+      while (i < src.size() && (std::isalnum(static_cast<unsigned char>(src[i])) || src[i] == '_')) {
+        t.text.push_back(src[i]);
+        bump();
+      }
+    } else if (std::isdigit(c)) {
+      t.kind = TokKind::Number;
+      while (i < src.size() && (std::isdigit(static_cast<unsigned char>(src[i])) || src[i] == '.')) {
+        t.text.push_back(src[i]);
+        bump();
+      }
+      t.value = std::stod(t.text);
+    } else if (c == '"') {
+      t.kind = TokKind::Text;
+      bump();
+      while (i < src.size() && src[i] != '"') {
+        t.text.push_back(src[i]);
+        bump();
+      }
+      if (i >= src.size()) throw std::runtime_error("lex:" + std::to_string(t.line) + ": unterminated string");
+      bump();
+    } else if (std::string("=,:?(){}<>").find(static_cast<char>(c)) != std::string::npos) {
+      t.kind = TokKind::Punct;
+      t.text = std::string(1, static_cast<char>(c));
+      bump();
+    } else {
+      throw std::runtime_error("lex:" + std::to_string(line) + ":" + std::to_string(col) + ": unexpected '" +
+                               std::string(1, static_cast<char>(c)) + "'");
+    }
+    out.push_back(std::move(t));
+  }
+}
+
+// ======================================================================= parser
+namespace {
+
+// Words the language reserves; they cannot name a tensor or a key.
+const std::set<std::string> &reserved() {
+  static const std::set<std::string> r{"target", "decode", "kvcache", "query", "decode_attn", "scale",
+                                       "auto",   "splits", "gqa_pack", "true", "false"};
+  return r;
+}
+
+class Reader {
+public:
+  explicit Reader(std::vector<Token> toks) : t_(std::move(toks)) {}
+
+  SourceFile file() {
+    SourceFile sf;
+    while (!atEnd()) {
+      if (isWord("target")) targetLine(sf);
+      else if (isWord("decode")) decode(sf);
+      else fail("expected 'target' or 'decode'");
+    }
+    if (!sf.has_decode) fail("program must contain a decode function");
+    return sf;
+  }
+
+private:
+  std::vector<Token> t_;
+  std::size_t p_ = 0;
+
+  const Token &cur() const { return t_[p_]; }
+  bool atEnd() const { return cur().kind == TokKind::End; }
+  bool isWord(const char *w) const { return cur().kind == TokKind::Word && cur().text == w; }
+  bool isPunct(char ch) const { return cur().kind == TokKind::Punct && cur().text[0] == ch; }
+  void next() {
+    if (!atEnd()) ++p_;
+  }
+
+  static std::string describe(const Token &t) {
+    switch (t.kind) {
+    case TokKind::End: return "end of input";
+    case TokKind::Number: return "number " + t.text;
+    case TokKind::Text: return "string \"" + t.text + "\"";
+    case TokKind::Punct: return "'" + t.text + "'";
+    case TokKind::Word: return reserved().count(t.text) ? "keyword '" + t.text + "'" : "'" + t.text + "'";
+    }
+    return "?";
+  }
+
+  [[noreturn]] void fail(const std::string &msg) const {
+    throw std::runtime_error("parse:" + std::to_string(cur().line) + ":" + std::to_string(cur().col) + ": " + msg);
+  }
+  void punct(char ch) {
+    if (!isPunct(ch)) fail(std::string("expected '") + ch + "', got " + describe(cur()));
+    next();
+  }
+  bool optPunct(char ch) {
+    if (!isPunct(ch)) return false;
+    next();
+    return true;
+  }
+  void keyword(const char *w) {
+    if (!isWord(w)) fail(std::string("expected '") + w + "', got " + describe(cur()));
+    next();
+  }
+  std::string name(const char *what) {
+    if (cur().kind != TokKind::Word || reserved().count(cur().text)) fail(std::string("expected ") + what);
+    std::string s = cur().text;
+    next();
+    return s;
+  }
+  double number(const char *what) {
+    if (cur().kind != TokKind::Number) fail(std::string("expected ") + what);
+    const double v = cur().value;
+    next();
+    return v;
+  }
+
+  void targetLine(SourceFile &sf) {
+    TargetLine t;
+    t.line = cur().line;
+    keyword("target");
+    t.key = name("target key");
+    punct('=');
+    if (cur().kind == TokKind::Number) {
+      t.number = cur().value;
+    } else if (cur().kind == TokKind::Text) {
+      t.quoted = true;
+      t.text = cur().text;
+    } else {
+      fail("expected number or quoted string");
+    }
+    next();
+    sf.targets.push_back(std::move(t));
+  }
+
+  int param(const char *want) {
+    if (!isWord(want)) fail(std::string("expected parameter ") + want);
+    next();
+    punct(':');
+    return static_cast<int>(number("integer"));
+  }
+
+  void decode(SourceFile &sf) {
+    if (sf.has_decode) fail("only one decode function is supported");
+    DecodeDecl fn;
+    keyword("decode");
+    fn.name = name("function name");
+    punct('(');
+    fn.H = param("H");
+    punct(',');
+    fn.H_kv = param("H_kv");
+    punct(',');
+    fn.d = param("d");
+    punct(',');
+    fn.n = param("n");
+    if (optPunct(',')) fn.batch = param("batch");
+    punct(')');
+    punct('{');
+    while (!isPunct('}') && !atEnd()) {
+      const int line = cur().line;
+      const std::string lhs = name("declaration or assignment name");
+      if (optPunct(':')) {
+        if (isWord("kvcache")) {
+          CacheDecl c = cache(fn);
+          c.name = lhs;
+          c.line = line;
+          fn.caches.push_back(std::move(c));
+        } else if (isWord("query")) {
+          fn.query = query();
+          fn.query.name = lhs;
+          fn.query.line = line;
+          fn.has_query = true;
+        } else {
+          fail("expected 'kvcache' or 'query'");
+        }
+      } else if (optPunct('=')) {
+        if (fn.has_attn) fail("only one decode_attn statement is supported");
+        fn.attn.out = lhs;
+        fn.attn.line = line;
+        attn(fn.attn);
+        fn.has_attn = true;
+      } else {
+        fail("expected ':' or '='");
+      }
+    }
+    punct('}');
+    if (fn.caches.size() != 2) fail("decode must declare exactly two caches (K and V)");
+    if (!fn.has_query) fail("decode must declare a query tensor");
+    if (!fn.has_attn) fail("decode must contain O = decode_attn(...)");
+    sf.decode = std::move(fn);
+    sf.has_decode = true;
+  }
+
+  TaggedWord tagged() {
+    TaggedWord w;
+    if (optPunct('?')) return w;
+    w.word = name("format or layout name");
+    if (optPunct(':')) w.arg = static_cast<int>(number("integer after ':'"));
+    return w;
+  }
+
+  static int dimension(const DecodeDecl &fn, const std::string &s, int line) {
+    if (s == "n") return fn.n;
+    if (s == "d") return fn.d;
+    if (s == "H") return fn.H;
+    if (s == "H_kv") return fn.H_kv;
+    try {
+      return std::stoi(s);
+    } catch (const std::exception &) {
+      throw std::runtime_error("semantic:" + std::to_string(line) + ": unknown dimension '" + s + "'");
+    }
+  }
+
+  CacheDecl cache(const DecodeDecl &fn) {
+    CacheDecl c;
+    c.line = cur().line;
+    keyword("kvcache");
+    punct('<');
+    auto dim = [&]() {
+      if (cur().kind != TokKind::Word && cur().kind != TokKind::Number) fail("expected shape dimension");
+      std::string s = cur().text;
+      next();
+      return s;
+    };
+    c.rows = dim();
+    punct(',');
+    c.cols = dim();
+    punct(',');
+    c.format = tagged();
+    punct(',');
+    c.order = tagged();
+    punct(',');
+    c.residency = tagged();
+    punct('>');
+    if (dimension(fn, c.rows, c.line) != fn.n || dimension(fn, c.cols, c.line) != fn.d)
+      throw std::runtime_error("semantic: cache shape must be <n, d, ...>");
+    return c;
+  }
+
+  QueryDeclaration query() {
+    QueryDeclaration q;
+    keyword("query");
+    punct('<');
+    q.rows = name("row dimension");
+    punct(',');
+    q.cols = name("column dimension");
+    punct(',');
+    q.dtype = name("dtype");
+    punct('>');
+    return q;
+  }
+
+  void attn(AttnCall &a) {
+    keyword("decode_attn");
+    punct('(');
+    a.q = name("query name");
+    punct(',');
+    a.k = name("key cache name");
+    punct(',');
+    a.v = name("value cache name");
+    while (optPunct(',')) {
+      if (isWord("scale")) {
+        next();
+        punct('=');
+        if (isWord("auto")) {
+          next();
+          a.scale_auto = true;
+        } else if (cur().kind == TokKind::Number) {
+          a.scale_auto = false;
+          a.scale = cur().value;
+          next();
+        } else {
+          fail("expected 'auto' or a number");
+        }
+      } else if (isWord("splits")) {
+        next();
+        punct('=');
+        if (optPunct('?')) {
+          a.splits = 0;
+        } else if (cur().kind == TokKind::Number) {
+          a.splits = static_cast<int>(cur().value);
+          if (a.splits < 1) fail("splits must be >= 1");
+          next();
+        } else {
+          fail("expected integer or '?'");
+        }
+      } else if (isWord("gqa_pack")) {
+        next();
+        punct('=');
+        if (optPunct('?')) {
+          a.gqa_pack = -1;
+        } else if (isWord("true") || isWord("false")) {
+          a.gqa_pack = isWord("true") ? 1 : 0;
+          next();
+        } else {
+          fail("expected true, false or '?'");
+        }
+      } else {
+        fail("expected scale=, splits= or gqa_pack=");
+      }
+    }
+    punct(')');
+  }
+};
+
+} // namespace
+
+SourceFile parseSource(const std::string &src) { return Reader(scanSource(src)).file(); }
+
+// ======================================================================= module
+int Module::add(const std::string &name, const ValueTy &ty) {
+  values.push_back(SsaValue{name, ty});
+  return static_cast<int>(values.size()) - 1;
+}
+
+const Operation &Module::attn() const {
+  for (const auto &o : ops)
+    if (o.op == Op::DecodeAttn || o.op == Op::DecodeAttnSplit) return o;
+  throw std::runtime_error("module has no attention op");
+}
+
+std::string ValueTy::str() const {
+  std::ostringstream o;
+  if (!cache) {
+    o << "tensor<" << rows << "x" << cols << "xf32>";
+  } else {
+    o << "kvcache<" << rows << "x" << cols << "x" << (fmt_free ? std::string("?") : fmt.str()) << ", "
+      << (layout_free ? std::string("?/?") : layout.str()) << ">";
+  }
+  return o.str();
+}
+
+namespace {
+
+// Format of one cache declaration; quantized formats default to group 128
+// and take groups of 32, 64 or 128 that divide d (src/ir.cpp:35-54).
+KvFormat resolveFormat(const CacheDecl &c, int d, bool &free_out) {
+  KvFormat f;
+  const Format parsed = parseFormat(c.format.word);
+  free_out = parsed == Format::Unset;
+  if (free_out) return f;
+  f.fmt = parsed;
+  if (f.isQuantized()) {
+    f.group = c.format.arg > 0 ? c.format.arg : 128;
+    f.metadata_bits = 32;
+    if (f.group != 32 && f.group != 64 && f.group != 128)
+      throw std::runtime_error("quantization group must be 32, 64 or 128");
+    if (f.group > d || d % f.group != 0) throw std::runtime_error("quantization group must divide d");
+  }
+  return f;
+}
+
+// Layout of one cache declaration; pages default to 64 tokens and take 16,
+// 32, 64 or 128 (src/ir.cpp:56-71).
+KvLayout resolveLayout(const CacheDecl &c, bool &free_out) {
+  KvLayout l;
+  const Order o = parseOrder(c.order.word);
+  const Residency r = parseResidency(c.residency.word);
+  free_out = o == Order::Unset || r == Residency::Unset;
+  if (free_out) return l;
+  l.order = o;
+  l.residency = r;
+  if (r == Residency::Paged) {
+    l.block_tokens = c.residency.arg > 0 ? c.residency.arg : 64;
+    if (l.block_tokens != 16 && l.block_tokens != 32 && l.block_tokens != 64 && l.block_tokens != 128)
+      throw std::runtime_error("paged block size must be 16, 32, 64 or 128");
+  }
+  return l;
+}
+
+} // namespace
+
+Module lowerSource(const SourceFile &sf) {
+  const DecodeDecl &fn = sf.decode;
+  Module m;
+  m.spec.name = fn.name;
+  m.spec.H = fn.H;
+  m.spec.H_kv = fn.H_kv;
+  m.spec.d = fn.d;
+  m.spec.n = fn.n;
+  m.spec.batch = fn.batch;
+
+  // target lines: files, search options, else one machine key each
+  for (const auto &t : sf.targets) {
+    if (t.key == "machine") {
+      if (!t.quoted) throw std::runtime_error("target machine must be a quoted path");
+      m.machine_file = t.text;
+      m.machine = loadMachine(t.text);
+    } else if (t.key == "calib") {
+      if (!t.quoted) throw std::runtime_error("target calib must be a quoted path");
+      m.calib_file = t.text;
+      m.calib = loadCalib(t.text);
+    } else if (t.key == "include_quantized") {
+      m.space.include_quantized = t.number != 0;
+    } else if (t.key == "max_splits") {
+      m.space.max_splits = static_cast<int>(t.number);
+    } else if (t.key == "max_rel_err") {
+      m.space.max_rel_err = t.number;
+    } else {
+      applyMachineKey(m.machine, t.key, t.number, t.text);
+    }
+  }
+  // an accuracy budget is what admits lossy formats
+  if (m.space.max_rel_err > 0) m.space.include_quantized = true;
+
+  const DecodeSpec &s = m.spec;
+  if (s.H <= 0 || s.H_kv <= 0 || s.d <= 0 || s.n <= 0) throw std::runtime_error("H, H_kv, d and n must be positive");
+  if (s.H % s.H_kv != 0) throw std::runtime_error("H must be a multiple of H_kv (GQA group size)");
+  if (s.d != 64 && s.d != 128) throw std::runtime_error("the kernels support d = 64 or d = 128");
+  if (s.batch < 1) throw std::runtime_error("batch must be >= 1");
+  if (m.machine.sms < 1) throw std::runtime_error("sms must be >= 1");
+  if (m.machine.bw_peak_gbs <= 0 || m.machine.bw_sm_gbs <= 0)
+    throw std::runtime_error("bandwidth parameters must be positive");
+
+  auto findCache = [&](const std::string &n) -> const CacheDecl * {
+    for (const auto &c : fn.caches)
+      if (c.name == n) return &c;
+    return nullptr;
+  };
+  const CacheDecl *kd = findCache(fn.attn.k);
+  const CacheDecl *vd = findCache(fn.attn.v);
+  if (!kd || !vd) throw std::runtime_error("decode_attn names a cache that was not declared");
+  if (fn.attn.q != fn.query.name)
+    throw std::runtime_error("decode_attn names an undeclared query '" + fn.attn.q + "'");
+  if (fn.query.rows != "H" || fn.query.cols != "d")
+    throw std::runtime_error("query must be declared as query<H, d, f32>");
+  if (fn.query.dtype != "f32") throw std::runtime_error("only f32 queries are supported");
+
+  bool kf_free = false, vf_free = false, kl_free = false, vl_free = false;
+  const KvFormat kf = resolveFormat(*kd, s.d, kf_free);
+  const KvFormat vf = resolveFormat(*vd, s.d, vf_free);
+  const KvLayout kl = resolveLayout(*kd, kl_free);
+  const KvLayout vl = resolveLayout(*vd, vl_free);
+  // K and V share one format and one layout
+  if (kf_free != vf_free) throw std::runtime_error("K and V must both pin a format or both leave it '?'");
+  if (kl_free != vl_free) throw std::runtime_error("K and V must both pin a layout or both leave it '?'");
+  if (!kf_free && kf.str() != vf.str()) throw std::runtime_error("K and V formats must match in this release");
+  if (!kl_free && kl.str() != vl.str()) throw std::runtime_error("K and V layouts must match in this release");
+
+  m.space.format_free = kf_free;
+  m.space.layout_free = kl_free;
+  m.space.pinned_fmt = kf;
+  m.space.pinned_layout = kl;
+  m.space.splits_free = fn.attn.splits == 0;
+  m.space.pinned_splits = fn.attn.splits > 0 ? fn.attn.splits : 1;
+  m.space.pack_free = fn.attn.gqa_pack < 0;
+  m.space.pinned_pack = fn.attn.gqa_pack == 1;
+  const int g = s.g();
+  if (!m.space.pack_free && m.space.pinned_pack && g != 2 && g != 4 && g != 8)
+    throw std::runtime_error("gqa_pack = true needs a group size of 2, 4 or 8 query heads per KV head");
+
+  ValueTy dense;
+  dense.rows = s.H;
+  dense.cols = s.d;
+  auto defining = [](Op kind, int result) {
+    Operation op;
+    op.op = kind;
+    op.result = result;
+    return op;
+  };
+  const int q = m.add(fn.query.name, dense);
+  m.ops.push_back(defining(Op::Query, q));
+  std::map<std::string, int> cache_id;
+  for (const auto &c : fn.caches) {
+    ValueTy ct;
+    ct.cache = true;
+    ct.rows = s.n;
+    ct.cols = s.d;
+    ct.fmt = resolveFormat(c, s.d, ct.fmt_free);
+    ct.layout = resolveLayout(c, ct.layout_free);
+    cache_id[c.name] = m.add(c.name, ct);
+    m.ops.push_back(defining(Op::KvCache, cache_id[c.name]));
+  }
+  const int o = m.add(fn.attn.out, dense);
+  Operation at;
+  at.op = Op::DecodeAttn;
+  at.args = {q, cache_id[fn.attn.k], cache_id[fn.attn.v]};
+  at.result = o;
+  at.scale = fn.attn.scale_auto ? 1.0f / std::sqrt(static_cast<float>(s.d)) : static_cast<float>(fn.attn.scale);
+  m.ops.push_back(at);
+  m.spec.scale = at.scale;
+  Operation out;
+  out.op = Op::Output;
+  out.args = {o};
+  m.ops.push_back(out);
+  return m;
+}
+
+std::string printModule(const Module &m) {
+  static const char *names[] = {"kvf.query", "kvf.kvcache", "kvf.decode_attn", "kvf.decode_attn_split",
+                                "kvf.output"};
+  std::ostringstream o;
+  const DecodeSpec &s = m.spec;
+  o << "kvf.func @" << s.name << " {H = " << s.H << ", H_kv = " << s.H_kv << ", g = " << s.g() << ", d = " << s.d
+    << ", n = " << s.n << ", batch = " << s.batch << "}\n";
+  for (const auto &op : m.ops) {
+    o << "  ";
+    if (op.result >= 0) o << "%" << m.values[op.result].name << " = ";
+    o << names[static_cast<int>(op.op)];
+    for (std::size_t i = 0; i < op.args.size(); ++i) o << (i ? ", %" : " %") << m.values[op.args[i]].name;
+    const int typed = op.result >= 0 ? op.result : (op.args.empty() ? -1 : op.args[0]);
+    if (typed >= 0) o << " : " << m.values[typed].ty.str();
+    if (op.op == Op::DecodeAttn || op.op == Op::DecodeAttnSplit) {
+      o << " {scale = " << op.scale;
+      if (op.planned) {
+        o << ", format = " << op.plan.fmt.str() << ", layout = " << op.plan.layout.str()
+          << ", splits = " << op.plan.part.splits << ", gqa_pack = " << (op.plan.part.gqa_pack ? "true" : "false")
+          << ", waves = " << op.plan.part.warps << ", unroll = " << op.plan.part.unroll
+          << ", workgroups = " << op.cost.blocks << ", pred_us = " << op.cost.t_total_us
+          << ", pred_gbs = " << op.cost.achieved_gbs;
+      }
+      o << "}";
+    }
+    o << "\n";
+  }
+  return o.str();
+}
+
+void planModule(Module &m) {
+  const std::vector<Plan> plans = enumeratePlans(m.spec, m.machine, m.space);
+  if (plans.empty()) throw std::runtime_error("planner: design space is empty");
+  m.ranked = rankPlans(m.spec, m.machine, m.calib, plans, m.space.max_rel_err);
+  const Ranked *pick = nullptr;
+  for (const auto &r : m.ranked)
+    if (!r.cost.rejected) {
+      pick = &r;
+      break;
+    }
+  if (!pick) throw std::runtime_error("planner: every candidate fails the accuracy limit (max_rel_err)");
+  bool done = false;
+  for (auto &op : m.ops) {
+    if (op.op != Op::DecodeAttn) continue;
+    op.op = Op::DecodeAttnSplit;
+    op.plan = pick->plan;
+    op.cost = pick->cost;
+    op.planned = true;
+    for (int id : op.args) {
+      ValueTy &t = m.values[id].ty;
+      if (!t.cache) continue;
+      t.fmt = pick->plan.fmt;
+      t.layout = pick->plan.layout;
+      t.fmt_free = t.layout_free = false;
+    }
+    done = true;
+  }
+  if (!done) throw std::runtime_error("planner: no kvf.decode_attn to plan");
+}
+
+} // namespace kvfc

@@ -1,0 +1,153 @@
+// kvf_front.h - front end of the kvf compiler: the .kv language, its module
+// form and the planner pass.
+//
+// The language is the reference's (docs/dsl.md; grammar as parsed by
+// src/parser.cpp:37-282), so existing .kv files compile unchanged:
+//
+//   target <key> = <number | "text">            (any number of these)
+//   decode <name>(H: N, H_kv: N, d: N, n: N [, batch: N]) {
+//     <Q>: query<H, d, f32>
+//     <K>: kvcache<n, d, FORMAT, ORDER, RESIDENCY>
+//     <V>: kvcache<n, d, FORMAT, ORDER, RESIDENCY>
+//     <O> = decode_attn(<Q>, <K>, <V> [, scale = auto|X] [, splits = N|?]
+//                       [, gqa_pack = true|false|?])
+//   }
+//
+// where FORMAT is `f16 | int8[:G] | int4[:G] | ?`, ORDER is
+// `head_major | token_major | ?` (an optional `:N` is accepted) and RESIDENCY
+// is `contiguous | paged[:B] | ?`; `?` leaves the choice to the planner.
+// Comments run from `#` or `//` to the end of the line.
+//
+// The module is a small SSA form with the reference's op names
+// (kvf.query, kvf.kvcache, kvf.decode_attn, kvf.decode_attn_split,
+// kvf.output); planning rewrites kvf.decode_attn into the split form and
+// types the caches with the chosen format and layout
+// (src/passes.cpp:7-47).
+#pragma once
+
+#include "kvf_model.h"
+
+#include <string>
+#include <vector>
+
+namespace kvfc {
+
+// ---------------------------------------------------------------- tokens
+enum class TokKind { End, Word, Number, Text, Punct };
+
+struct Token {
+  TokKind kind = TokKind::End;
+  std::string text; // word, digits, string contents or the punctuation char
+  double value = 0; // numbers
+  int line = 1, col = 1;
+};
+
+// Whole-source scan; throws "lex:L:C: ..." on a character outside the language.
+std::vector<Token> scanSource(const std::string &src);
+
+// ---------------------------------------------------------------- syntax
+// As written in the source; `?` and defaults are resolved when lowering.
+struct TargetLine {
+  std::string key;
+  bool quoted = false;
+  double number = 0;
+  std::string text;
+  int line = 1;
+};
+
+struct TaggedWord { // `int8:64`, `paged:16`, `?`
+  std::string word = "?";
+  int arg = 0;
+};
+
+struct CacheDecl {
+  std::string name;
+  std::string rows, cols;
+  TaggedWord format, order, residency;
+  int line = 1;
+};
+
+struct QueryDeclaration {
+  std::string name, rows, cols, dtype;
+  int line = 1;
+};
+
+struct AttnCall {
+  std::string out, q, k, v;
+  bool scale_auto = true;
+  double scale = 0;
+  int splits = 0; // 0: free
+  int gqa_pack = -1; // -1 free, 0 false, 1 true
+  int line = 1;
+};
+
+struct DecodeDecl {
+  std::string name;
+  int H = 0, H_kv = 0, d = 0, n = 0, batch = 1;
+  std::vector<CacheDecl> caches;
+  QueryDeclaration query;
+  AttnCall attn;
+  bool has_query = false, has_attn = false;
+};
+
+struct SourceFile {
+  std::vector<TargetLine> targets;
+  DecodeDecl decode;
+  bool has_decode = false;
+};
+
+// Throws "parse:L:C: ..." for syntax errors, "semantic: ..." for a cache
+// shape other than <n, d>.
+SourceFile parseSource(const std::string &src);
+
+// ---------------------------------------------------------------- module
+enum class Op { Query, KvCache, DecodeAttn, DecodeAttnSplit, Output };
+
+struct ValueTy {
+  bool cache = false;
+  int rows = 0, cols = 0;
+  KvFormat fmt;
+  KvLayout layout;
+  bool fmt_free = false, layout_free = false;
+  std::string str() const;
+};
+
+struct SsaValue {
+  std::string name;
+  ValueTy ty;
+};
+
+struct Operation {
+  Op op = Op::Query;
+  std::vector<int> args;
+  int result = -1;
+  float scale = 0;
+  bool planned = false;
+  Plan plan;
+  Cost cost;
+};
+
+struct Module {
+  DecodeSpec spec;
+  Machine machine;
+  Calib calib = Calib::defaults();
+  SearchSpace space;
+  std::string machine_file, calib_file;
+  std::vector<SsaValue> values;
+  std::vector<Operation> ops;
+  std::vector<Ranked> ranked; // every candidate, cheapest first
+  int add(const std::string &name, const ValueTy &ty);
+  const Operation &attn() const;
+};
+
+// Semantic analysis (src/ir.cpp:82-236): resolve the signature, apply the
+// target lines, check the declarations and fold every `?` into the search
+// space.
+Module lowerSource(const SourceFile &sf);
+std::string printModule(const Module &m);
+
+// Enumerate, rank, keep the cheapest plan that passes the accuracy gate and
+// rewrite the attention op with it.
+void planModule(Module &m);
+
+} // namespace kvfc

@@ -1,0 +1,253 @@
+"""The kvf compiler (kvforge_amd/bin/kvf) against the reference's own outputs.
+
+Golden data (tests/golden/compiler, copied by tests/golden/make_fixtures.py):
+plans.csv of the four edge shapes (results/edge/*), the full prediction table
+of the reference's RTX 5060 sweep under its fitted constants, and the
+constants plus the report that calibrating on that sweep produced. Front-end
+behaviour follows the reference's tests/smoke.ps1: the semantic checks and
+the nine rejection messages. Where the reference compiler has been built
+from its sources (oracle/_ref/kvf_ref), further programs are compared with it
+byte for byte.
+"""
+import gzip
+import os
+import subprocess
+
+import pytest
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+KVF = os.path.join(ROOT, "kvforge_amd", "bin", "kvf")
+REF = os.path.join(ROOT, "oracle", "_ref", "kvf_ref")
+GOLD = os.path.join(ROOT, "tests", "golden", "compiler")
+GEN = os.path.join(ROOT, "kvforge_amd", "csrc", "gen")
+
+
+@pytest.fixture(scope="module", autouse=True)
+def _built():
+    subprocess.run(["make", "-s", "-C", os.path.join(ROOT, "kvforge_amd"), KVF], check=True)
+
+
+def kvf(*args, cwd=None, exe=KVF):
+    return subprocess.run([exe, *args], cwd=cwd, capture_output=True, text=True)
+
+
+def spec(name, H, Hkv, d, n, batch=1, fmt="?", order="?", res="?", splits="?", pack="?",
+         targets=()):
+    lines = list(targets)
+    lines.append(f"decode {name}(H: {H}, H_kv: {Hkv}, d: {d}, n: {n}, batch: {batch}) {{")
+    lines.append("  Q: query<H, d, f32>")
+    lines.append(f"  K: kvcache<n, d, {fmt}, {order}, {res}>")
+    lines.append(f"  V: kvcache<n, d, {fmt}, {order}, {res}>")
+    lines.append(f"  O = decode_attn(Q, K, V, scale = auto, splits = {splits}, gqa_pack = {pack})")
+    lines.append("}")
+    return "\n".join(lines) + "\n"
+
+
+def write(tmp_path, name, text):
+    p = tmp_path / name
+    p.write_text(text)
+    return str(p)
+
+
+def machine(name):
+    return os.path.join(GOLD, name)
+
+
+# ---------------------------------------------------------------- golden plans
+# the reference's tests/edge/*.kv shapes (rtx5060 machine, lossy formats on)
+EDGE = {
+    "edge_g8_n3333": (16, 2, 64, 3333, 3),
+    "edge_n129": (32, 8, 128, 129, 1),
+    "edge_odd_n": (12, 4, 128, 1001, 2),
+    "edge_short": (8, 8, 64, 100, 1),
+}
+
+
+@pytest.mark.parametrize("name", sorted(EDGE))
+def test_edge_plans_csv_matches_reference(tmp_path, name):
+    H, Hkv, d, n, b = EDGE[name]
+    src = write(tmp_path, f"{name}.kv", spec(
+        name, H, Hkv, d, n, b,
+        targets=[f'target machine = "{machine("rtx5060-laptop.gpu")}"',
+                 "target include_quantized = 1"]))
+    r = kvf("plan", src, "--out", str(tmp_path / "out"), "--top", "3")
+    assert r.returncode == 0, r.stderr
+    got = (tmp_path / "out" / "plans.csv").read_bytes()
+    want = open(os.path.join(GOLD, f"{name}_plans.csv"), "rb").read()
+    assert got == want
+
+
+def test_predict_matches_reference_table(tmp_path):
+    sweep = tmp_path / "sweep.csv"
+    sweep.write_bytes(gzip.open(os.path.join(GOLD, "sweep_rtx5060-laptop.csv.gz")).read())
+    out = tmp_path / "pred.csv"
+    r = kvf("predict", "--sweep", str(sweep), "--machine", machine("rtx5060-laptop.gpu"),
+            "--calib", os.path.join(GOLD, "constants_rtx5060.cal"), "--out", str(out))
+    assert r.returncode == 0, r.stderr
+    want = gzip.open(os.path.join(GOLD, "predicted_full_rtx5060-laptop.csv.gz")).read()
+    assert out.read_bytes() == want
+
+
+def test_calibrate_reproduces_reference_constants(tmp_path):
+    sweep = tmp_path / "sweep.csv"
+    sweep.write_bytes(gzip.open(os.path.join(GOLD, "sweep_rtx5060-laptop.csv.gz")).read())
+    cal = tmp_path / "fit.cal"
+    r = kvf("calibrate", "--sweep", str(sweep), "--machine", machine("rtx5060-laptop.gpu"),
+            "--out", str(cal))
+    assert r.returncode == 0, r.stderr
+    assert cal.read_text() == open(os.path.join(GOLD, "constants_rtx5060.cal")).read()
+    # the printed report (fitted constants, then metrics on the fitted and the
+    # held-out shapes) is the reference's too
+    want = open(os.path.join(GOLD, "calibrate_rtx5060.txt"), encoding="utf-8-sig").read()
+    assert r.stdout == want.replace("\r\n", "\n")
+
+
+# ---------------------------------------------------------------- front end
+GEN_HDR = f'target machine = "{os.path.join(GOLD, "generic-gpu.gpu")}"'
+
+
+def test_pinned_splits_honoured_with_pack_free(tmp_path):
+    src = write(tmp_path, "p.kv", spec("served_gqa", 32, 8, 128, 8192, 8, fmt="f16",
+                                       splits=4, targets=[GEN_HDR]))
+    r = kvf("plan", src, "--out", str(tmp_path / "o"), "--top", "400")
+    assert r.returncode == 0, r.stderr
+    assert "splits=4" in r.stdout and "splits=1 " not in r.stdout and "splits=8" not in r.stdout
+    rows = (tmp_path / "o" / "plans.csv").read_text().splitlines()[1:]
+    assert rows and all(row.split(",")[11] == "4" for row in rows)
+    assert {row.split(",")[12] for row in rows} == {"0", "1"}
+
+
+def test_accuracy_limit_keeps_int4_out(tmp_path):
+    src = write(tmp_path, "l.kv", spec("llama3_8b", 32, 8, 128, 32768, targets=[GEN_HDR]))
+    r = kvf("plan", src, "--out", str(tmp_path / "o"), "--max-err", "0.02", "--top", "3")
+    assert r.returncode == 0, r.stderr
+    chosen = [ln for ln in r.stdout.splitlines() if ln.strip().startswith("format:")][0]
+    assert "int8" in chosen
+
+
+def test_lossy_formats_excluded_by_default(tmp_path):
+    src = write(tmp_path, "p.kv", spec("served_gqa", 32, 8, 128, 8192, 8, fmt="f16",
+                                       splits=4, targets=[GEN_HDR]))
+    r = kvf("plan", src, "--out", str(tmp_path / "o"), "--top", "3")
+    assert r.returncode == 0 and "lossy formats excluded" in r.stdout
+
+
+def _body(H, Hkv, d, kfmt="f16", vfmt=None, kshape="n, d", extra="", v="V"):
+    vfmt = vfmt or kfmt
+    return (f"decode bad(H: {H}, H_kv: {Hkv}, d: {d}, n: 1024) {{ Q: query<H, d, f32> "
+            f"K: kvcache<{kshape}, {kfmt}> V: kvcache<n, d, {vfmt}> "
+            f"O = decode_attn(Q, K, {v}{extra}) }}")
+
+
+TM = "token_major, contiguous"
+REJECT = [
+    ("h_multiple", GEN_HDR + "\n" + _body(30, 8, 128, f"f16, {TM}"), "multiple of H_kv"),
+    ("typo_key", "target bw_peek_gbs = 40\n" + _body(8, 8, 128, f"f16, {TM}"), "unknown machine key"),
+    ("format_name", GEN_HDR + "\n" + _body(8, 8, 128, f"fp16, {TM}"), "unknown KV format"),
+    ("cache_shape", GEN_HDR + "\n" + _body(8, 8, 128, f"f16, {TM}", kshape="n, 64"), "cache shape"),
+    ("free_mismatch", GEN_HDR + "\n" + _body(8, 8, 128, f"f16, {TM}", vfmt="?, ?, ?"),
+     "both pin a format"),
+    ("undeclared", GEN_HDR + "\n" + _body(8, 8, 128, f"f16, {TM}", v="W"), "not declared"),
+    ("head_dim", GEN_HDR + "\n" + _body(8, 8, 96, f"f16, {TM}"), "d = 64 or d = 128"),
+    ("group_divides", GEN_HDR + "\n" + _body(8, 8, 64, f"int8:128, {TM}"), "divide d"),
+    ("pack_group", GEN_HDR + "\n" + _body(24, 8, 128, f"f16, {TM}", extra=", gqa_pack = true"),
+     "gqa_pack = true needs"),
+]
+
+
+@pytest.mark.parametrize("case,text,needle", REJECT, ids=[c[0] for c in REJECT])
+def test_rejections(tmp_path, case, text, needle):
+    r = kvf("plan", write(tmp_path, f"{case}.kv", text), "--out", str(tmp_path / "o"))
+    assert r.returncode != 0
+    assert needle in r.stderr, r.stderr
+
+
+def test_syntax_errors_name_the_position(tmp_path):
+    r = kvf("plan", write(tmp_path, "s.kv", "decode x(H: 8, H_kv: 8, d: 128 n: 4) {}"))
+    assert r.returncode == 1 and "parse:1:" in r.stderr
+    r = kvf("plan", write(tmp_path, "t.kv", "decode x(H: 8, H_kv: 8, d: 128, n: 4) { Q: query<H, d, f32> $ }"))
+    assert r.returncode == 1 and "lex:1:" in r.stderr
+
+
+def test_machine_files_load():
+    for f in ("generic-gpu.gpu", "rtx5060-laptop.gpu", "rtx4060-laptop.gpu"):
+        r = kvf("machine", machine(f))
+        assert r.returncode == 0 and "cost model     = warp" in r.stdout
+    r = kvf("machine", os.path.join(ROOT, "machines", "mi355x.gpu"))
+    assert r.returncode == 0 and "cost model     = cdna" in r.stdout and "sms = 256" in r.stdout
+
+
+# ---------------------------------------------------------------- against the built reference
+REF_PROGRAMS = {
+    "llama3_gate": (spec("llama3_8b", 32, 8, 128, 32768, targets=[GEN_HDR, "target max_rel_err = 0.02"]), []),
+    "mha_budget": (spec("mha_4k", 32, 32, 128, 4096, targets=[GEN_HDR, "target max_rel_err = 0.1"]), []),
+    "pinned": (spec("baseline_fp16", 32, 8, 128, 32768, fmt="f16", order="token_major", res="contiguous",
+                    splits=1, pack="false", targets=[GEN_HDR]), []),
+    "paged_long": (spec("long_ctx", 32, 8, 128, 65536, fmt="int4:32", order="head_major", res="paged:16",
+                        targets=[f'target machine = "{machine("rtx4060-laptop.gpu")}"',
+                                 "target max_splits = 256"]), []),
+    "overrides": (spec("tweak", 64, 8, 64, 20000, 3, targets=[GEN_HDR, "target sms = 20",
+                                                               "target include_quantized = 1"]),
+                  ["--calib", os.path.join(GOLD, "constants_rtx5060.cal")]),
+}
+
+
+@pytest.mark.skipif(not os.path.exists(REF), reason="reference compiler not built (oracle/_ref)")
+@pytest.mark.parametrize("name", sorted(REF_PROGRAMS))
+def test_plans_csv_matches_built_reference(tmp_path, name):
+    text, extra = REF_PROGRAMS[name]
+    src = write(tmp_path, f"{name}.kv", text)
+    a = kvf("plan", src, "--out", str(tmp_path / "ours"), *extra)
+    b = kvf("plan", src, "--out", str(tmp_path / "ref"), *extra, exe=REF)
+    assert a.returncode == 0 and b.returncode == 0, (a.stderr, b.stderr)
+    assert (tmp_path / "ours" / "plans.csv").read_bytes() == (tmp_path / "ref" / "plans.csv").read_bytes()
+    hdr_ours = (tmp_path / "ours" / "plan_info.h").read_text()
+    hdr_ref = (tmp_path / "ref" / "plan_info.h").read_text()
+    assert hdr_ours == hdr_ref
+
+
+# ---------------------------------------------------------------- code generation
+def test_emit_dispatch_reproduces_library_sources(tmp_path):
+    r = kvf("emit-dispatch", "--out", str(tmp_path), "--d", "128,64", "--g", "1,2,4,8")
+    assert r.returncode == 0, r.stderr
+    ours = sorted(os.listdir(tmp_path))
+    assert ours == sorted(os.listdir(GEN))
+    for f in ours:
+        assert (tmp_path / f).read_text() == open(os.path.join(GEN, f)).read(), f
+
+
+def test_plan_emits_hip_launcher(tmp_path):
+    src = write(tmp_path, "ns.kv", spec(
+        "north_star", 32, 8, 128, 32768, fmt="int8:64", order="head_major", res="contiguous",
+        targets=[f'target machine = "{os.path.join(ROOT, "machines", "mi355x.gpu")}"']))
+    r = kvf("plan", src, "--out", str(tmp_path / "o"))
+    assert r.returncode == 0, r.stderr
+    tu = (tmp_path / "o" / "decode_north_star.hip").read_text()
+    assert 'extern "C" hipError_t kvf_launch_north_star(const kvf::Args *in, hipStream_t st)' in tu
+    assert 'extern "C" const char *kvf_plan_north_star()' in tu
+    assert "a.group_shift = 6;" in tu and "kvf::launch<kvf::FMT_INT8, 128," in tu
+    assert "cuda" not in tu.lower()
+    plan = [ln for ln in tu.splitlines() if ln.startswith("// plan: ")][0][len("// plan: "):]
+    assert f'return "{plan}";' in tu
+
+
+HIPCC = "/opt/rocm/bin/hipcc"
+
+
+@pytest.mark.skipif(not os.path.exists(HIPCC), reason="hipcc not installed")
+def test_generated_launcher_compiles_for_gfx950(tmp_path):
+    src = write(tmp_path, "pg.kv", spec(
+        "paged_tm", 32, 8, 128, 8192, 8, fmt="int4:32", order="token_major", res="paged:16",
+        targets=[f'target machine = "{os.path.join(ROOT, "machines", "mi355x.gpu")}"']))
+    r = kvf("plan", src, "--out", str(tmp_path / "o"))
+    assert r.returncode == 0, r.stderr
+    obj = tmp_path / "o" / "tu.o"
+    c = subprocess.run([HIPCC, "-std=c++17", "-O3", "--offload-arch=gfx950", "-fPIC",
+                        "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+                        "-I", os.path.join(ROOT, "include"),
+                        "-I", os.path.join(ROOT, "kvforge_amd", "csrc"),
+                        "-c", str(tmp_path / "o" / "decode_paged_tm.hip"), "-o", str(obj)],
+                       capture_output=True, text=True)
+    assert c.returncode == 0, c.stderr[-2000:]
+    syms = subprocess.run(["nm", str(obj)], capture_output=True, text=True).stdout
+    assert " T kvf_launch_paged_tm" in syms and " T kvf_plan_paged_tm" in syms
