@@ -1,0 +1,457 @@
+// sweep - times every plan of a design space on one MI355X and checks each
+// against a double-precision reference; the measurements the cost model is
+// fitted and judged on.
+//
+// Behaviour follows the reference's bench/sweep.cu:95-215:
+//   input   plans.csv files written by `kvf plan <shape.kv> --all` (one shape
+//           per file, one row per candidate);
+//   data    q, K, V from make_data(seed) (std::mt19937_64 +
+//           std::normal_distribution<float>, runtime/kvf_host.h:51-61), page
+//           tables from seed + 17;
+//   check   err_ref = rel_l2(out, exact attention over the dequantised
+//           cache) must be < 2e-3; err_exact is against the fp32 inputs;
+//   timing  per rep: flush, event, launch (split kernel + merge), event;
+//           median / p25 / p75 / min over the reps;
+//   output  the reference's sweep CSV columns.
+// MI355X specifics: the cache is quantized and placed on the GPU by the
+// library's own kvf_quantize_place (bit-exact with the reference's host
+// quantizer); the flush writes 512 MiB, twice the 256 MiB MALL, so no rep
+// finds the cache in the memory-side cache; `warps` are 64-lane wavefronts.
+//
+//   kvf_sweep --plans a.csv[,b.csv] --out sweep.csv
+//             [--reps 25] [--warmup 5] [--seed 1] [--limit N] [--device 0]
+//             [--threads T]
+#include "kvf_abi.h"
+
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cmath>
+#include <cstdint>
+#include <cstdio>
+#include <cstdlib>
+#include <cstring>
+#include <fstream>
+#include <map>
+#include <numeric>
+#include <random>
+#include <sstream>
+#include <string>
+#include <thread>
+#include <tuple>
+#include <vector>
+
+extern "C" {
+void kvfh_make_data(int B, int H, int Hkv, int D, int n, uint64_t seed, float *q, float *K, float *V);
+void kvfh_page_table(long long pages, uint64_t seed, int32_t *out);
+}
+
+namespace {
+
+#define CHECK(x)                                                                                   \
+  do {                                                                                             \
+    hipError_t e_ = (x);                                                                           \
+    if (e_ != hipSuccess) {                                                                        \
+      std::fprintf(stderr, "%s:%d: %s failed: %s\n", __FILE__, __LINE__, #x, hipGetErrorString(e_)); \
+      std::exit(1);                                                                                \
+    }                                                                                              \
+  } while (0)
+
+std::vector<std::string> fields(const std::string &s, char sep) {
+  std::vector<std::string> out(1);
+  for (char c : s) {
+    if (c == sep) out.emplace_back();
+    else if (c != '\r') out.back().push_back(c);
+  }
+  return out;
+}
+
+struct PlanRow {
+  std::string name, fmt, order, residency;
+  int H = 0, Hkv = 0, D = 0, n = 0, batch = 0, group = 0, bt = 0, splits = 1, pack = 0, warps = 4, unroll = 2;
+};
+
+std::vector<PlanRow> readPlans(const std::string &path) {
+  std::ifstream in(path);
+  if (!in) {
+    std::fprintf(stderr, "cannot read %s\n", path.c_str());
+    std::exit(2);
+  }
+  std::string line;
+  std::getline(in, line);
+  std::map<std::string, size_t> col;
+  const auto head = fields(line, ',');
+  for (size_t i = 0; i < head.size(); ++i) col[head[i]] = i;
+  std::vector<PlanRow> rows;
+  while (std::getline(in, line)) {
+    if (line.empty()) continue;
+    const auto f = fields(line, ',');
+    auto S = [&](const char *k) { return f.at(col.at(k)); };
+    auto I = [&](const char *k) { return std::stoi(S(k)); };
+    PlanRow r;
+    r.name = S("name");
+    r.H = I("H");
+    r.Hkv = I("H_kv");
+    r.D = I("d");
+    r.n = I("n");
+    r.batch = I("batch");
+    r.fmt = S("fmt");
+    r.group = I("group");
+    r.order = S("order");
+    r.residency = S("residency");
+    r.bt = I("block_tokens");
+    r.splits = I("splits");
+    r.pack = I("gqa_pack");
+    r.warps = I("warps");
+    r.unroll = I("unroll");
+    rows.push_back(r);
+  }
+  return rows;
+}
+
+int fmtCode(const std::string &f) { return f == "f16" ? 0 : f == "int8" ? 1 : 2; }
+int bitsOf(int fmt) { return fmt == 0 ? 16 : fmt == 1 ? 8 : 4; }
+
+std::string variantOf(const PlanRow &p) {
+  return p.fmt + (p.order == "head_major" ? "_hm" : "_tm") + (p.residency == "paged" ? "_p" : "_c") + "_g" +
+         std::to_string(p.pack ? p.H / p.Hkv : 1) + "_u" + std::to_string(p.unroll) + "_d" + std::to_string(p.D);
+}
+
+// IEEE binary16 -> binary32, exact.
+float halfBits(uint16_t h) {
+  const uint32_t s = (h >> 15) & 1, e = (h >> 10) & 31, m = h & 1023;
+  float v;
+  if (e == 0) v = std::ldexp(static_cast<float>(m), -24);
+  else if (e == 31) v = m ? NAN : INFINITY;
+  else v = std::ldexp(static_cast<float>(m | 1024), static_cast<int>(e) - 25);
+  return s ? -v : v;
+}
+
+// Values a cache of `rows` rows holds after quantization: codes (f16 payload
+// or int8/int4 codes) times the group scale plus the group zero.
+std::vector<float> dequantise(int fmt, int group, int D, long long rows, const std::vector<uint8_t> &data,
+                              const std::vector<uint32_t> &meta) {
+  std::vector<float> out(static_cast<size_t>(rows) * D);
+  const long long rb = D * bitsOf(fmt) / 8;
+  const int gpr = fmt == 0 ? 0 : D / group;
+  for (long long r = 0; r < rows; ++r) {
+    const uint8_t *row = data.data() + r * rb;
+    for (int c = 0; c < D; ++c) {
+      float x;
+      if (fmt == 0) {
+        uint16_t h;
+        std::memcpy(&h, row + 2 * c, 2);
+        x = halfBits(h);
+      } else {
+        const int code = fmt == 1 ? row[c] : (c & 1 ? row[c / 2] >> 4 : row[c / 2] & 15);
+        const uint32_t w = meta[r * gpr + c / group];
+        const float scale = halfBits(static_cast<uint16_t>(w & 0xffff));
+        const float zero = halfBits(static_cast<uint16_t>(w >> 16));
+        x = static_cast<float>(code) * scale + zero;
+      }
+      out[r * D + c] = x;
+    }
+  }
+  return out;
+}
+
+// Exact attention in double over logical [B][Hkv][n][D] K and V, one thread
+// per slice of (b, h) pairs.
+std::vector<float> attention(int B, int H, int Hkv, int D, int n, const std::vector<float> &q,
+                             const std::vector<float> &K, const std::vector<float> &V, float scale, int threads) {
+  std::vector<float> out(static_cast<size_t>(B) * H * D);
+  const int g = H / Hkv;
+  auto work = [&](int first, int step) {
+    std::vector<double> s(n), acc(D);
+    for (int bh = first; bh < B * H; bh += step) {
+      const int b = bh / H, h = bh % H, hk = h / g;
+      const float *qv = &q[static_cast<size_t>(bh) * D];
+      const size_t base = (static_cast<size_t>(b) * Hkv + hk) * n * D;
+      double mx = -INFINITY;
+      for (int t = 0; t < n; ++t) {
+        double dot = 0;
+        for (int c = 0; c < D; ++c) dot += static_cast<double>(qv[c]) * K[base + static_cast<size_t>(t) * D + c];
+        s[t] = dot * scale;
+        mx = std::max(mx, s[t]);
+      }
+      double sum = 0;
+      std::fill(acc.begin(), acc.end(), 0.0);
+      for (int t = 0; t < n; ++t) {
+        const double p = std::exp(s[t] - mx);
+        sum += p;
+        for (int c = 0; c < D; ++c) acc[c] += p * V[base + static_cast<size_t>(t) * D + c];
+      }
+      for (int c = 0; c < D; ++c) out[static_cast<size_t>(bh) * D + c] = static_cast<float>(acc[c] / sum);
+    }
+  };
+  std::vector<std::thread> pool;
+  for (int t = 0; t < threads; ++t) pool.emplace_back(work, t, threads);
+  for (auto &t : pool) t.join();
+  return out;
+}
+
+double relL2(const std::vector<float> &a, const std::vector<float> &ref) {
+  double num = 0, den = 0;
+  for (size_t i = 0; i < a.size(); ++i) {
+    const double d = static_cast<double>(a[i]) - ref[i];
+    num += d * d;
+    den += static_cast<double>(ref[i]) * ref[i];
+  }
+  return den > 0 ? std::sqrt(num / den) : std::sqrt(num);
+}
+
+struct Stats {
+  double median = 0, p25 = 0, p75 = 0, min = 0;
+  int reps = 0;
+};
+
+// One device cache in a plan's format and layout.
+struct DeviceCache {
+  uint8_t *k = nullptr, *v = nullptr;
+  uint32_t *km = nullptr, *vm = nullptr;
+  int32_t *table = nullptr;
+  int max_blocks = 0;
+  void release() {
+    for (void *p : {(void *)k, (void *)v, (void *)km, (void *)vm, (void *)table})
+      if (p) CHECK(hipFree(p));
+    *this = DeviceCache{};
+  }
+};
+
+} // namespace
+
+int main(int argc, char **argv) {
+  std::string plans_arg, out_path = "sweep.csv";
+  int reps = 25, warmup = 5, limit = 0, dev = 0;
+  int threads = static_cast<int>(std::min(16u, std::max(1u, std::thread::hardware_concurrency())));
+  uint64_t seed = 1;
+  for (int i = 1; i < argc; ++i) {
+    const std::string a = argv[i];
+    auto next = [&]() -> std::string {
+      if (i + 1 >= argc) {
+        std::fprintf(stderr, "%s needs a value\n", a.c_str());
+        std::exit(2);
+      }
+      return argv[++i];
+    };
+    if (a == "--plans") plans_arg = next();
+    else if (a == "--out") out_path = next();
+    else if (a == "--reps") reps = std::stoi(next());
+    else if (a == "--warmup") warmup = std::stoi(next());
+    else if (a == "--limit") limit = std::stoi(next());
+    else if (a == "--seed") seed = std::stoull(next());
+    else if (a == "--device") dev = std::stoi(next());
+    else if (a == "--threads") threads = std::max(1, std::stoi(next()));
+    else {
+      std::fprintf(stderr, "unknown option %s\n", a.c_str());
+      return 2;
+    }
+  }
+  if (plans_arg.empty() || reps < 1) {
+    std::fprintf(stderr, "usage: kvf_sweep --plans plans.csv[,more.csv] --out sweep.csv [--reps N]\n");
+    return 2;
+  }
+  CHECK(hipSetDevice(dev));
+  hipDeviceProp_t prop;
+  CHECK(hipGetDeviceProperties(&prop, dev));
+  std::string device = prop.name;
+  std::replace(device.begin(), device.end(), ',', ' ');
+  std::printf("device %s (%s, %d CUs), %d reference threads\n", device.c_str(), prop.gcnArchName,
+              prop.multiProcessorCount, threads);
+  std::printf("registry: %d variants\n", kvf_variant_count());
+
+  // 512 MiB flush region: twice the MALL, written before every timed rep
+  const size_t flush_bytes = 512ull << 20;
+  void *flush = nullptr;
+  CHECK(hipMalloc(&flush, flush_bytes));
+  hipStream_t st;
+  CHECK(hipStreamCreate(&st));
+  hipEvent_t e0, e1;
+  CHECK(hipEventCreate(&e0));
+  CHECK(hipEventCreate(&e1));
+
+  FILE *out = std::fopen(out_path.c_str(), "w");
+  if (!out) {
+    std::fprintf(stderr, "cannot write %s\n", out_path.c_str());
+    return 1;
+  }
+  std::fprintf(out, "name,H,H_kv,d,n,batch,fmt,group,order,residency,block_tokens,splits,gqa_pack,warps,unroll,"
+                    "t_us,t_p25,t_p75,t_min,reps,err_exact,err_ref,verified,device\n");
+  long long done = 0, skipped = 0, unverified = 0;
+
+  for (const std::string &pf : fields(plans_arg, ',')) {
+    std::vector<PlanRow> plans = readPlans(pf);
+    if (plans.empty()) continue;
+    if (limit > 0 && static_cast<int>(plans.size()) > limit) plans.resize(limit);
+    const PlanRow &p0 = plans[0];
+    const int B = p0.batch, H = p0.H, Hkv = p0.Hkv, D = p0.D, n = p0.n;
+    const long long rows = 1LL * B * Hkv * n;
+    std::printf("\nshape %s: B=%d H=%d Hkv=%d D=%d n=%d, %zu plans\n", p0.name.c_str(), B, H, Hkv, D, n,
+                plans.size());
+    std::fflush(stdout);
+
+    std::vector<float> q(static_cast<size_t>(B) * H * D), K(static_cast<size_t>(rows) * D),
+        V(static_cast<size_t>(rows) * D);
+    kvfh_make_data(B, H, Hkv, D, n, seed, q.data(), K.data(), V.data());
+    const float scale = 1.0f / std::sqrt(static_cast<float>(D));
+    const float scale_log2 = scale * 1.4426950408889634f;
+    const std::vector<float> exact = attention(B, H, Hkv, D, n, q, K, V, scale, threads);
+
+    float *dq, *dK, *dV, *dout, *dpo, *dpm;
+    int max_splits = 1;
+    for (const auto &p : plans) max_splits = std::max(max_splits, p.splits);
+    CHECK(hipMalloc(&dq, q.size() * 4));
+    CHECK(hipMalloc(&dK, K.size() * 4));
+    CHECK(hipMalloc(&dV, V.size() * 4));
+    CHECK(hipMalloc(&dout, q.size() * 4));
+    CHECK(hipMalloc(&dpo, static_cast<size_t>(B) * H * max_splits * D * 4));
+    CHECK(hipMalloc(&dpm, static_cast<size_t>(B) * H * max_splits * 2 * 4));
+    CHECK(hipMemcpy(dq, q.data(), q.size() * 4, hipMemcpyHostToDevice));
+    CHECK(hipMemcpy(dK, K.data(), K.size() * 4, hipMemcpyHostToDevice));
+    CHECK(hipMemcpy(dV, V.data(), V.size() * 4, hipMemcpyHostToDevice));
+    std::vector<float> got(q.size());
+
+    // plans grouped so each (format, layout) cache is built once, formats in order
+    std::map<std::tuple<std::string, int, std::string, std::string, int>, std::vector<size_t>> groups;
+    for (size_t i = 0; i < plans.size(); ++i) {
+      const auto &p = plans[i];
+      groups[{p.fmt, p.group, p.order, p.residency, p.bt}].push_back(i);
+    }
+    std::string cur_fmt;
+    std::vector<float> ref;
+    for (auto &[key, members] : groups) {
+      const PlanRow &pg = plans[members[0]];
+      const int fmt = fmtCode(pg.fmt), group = fmt == 0 ? 0 : pg.group;
+      const int row_bytes = D * bitsOf(fmt) / 8, meta_words = fmt == 0 ? 0 : D / group;
+      const bool paged = pg.residency == "paged";
+      const int order = pg.order == "head_major" ? 0 : 1, bt = paged ? pg.bt : 0;
+      const std::string fkey = pg.fmt + ":" + std::to_string(group);
+
+      if (fkey != cur_fmt) {
+        // the dequantised cache: quantize in logical (head-major contiguous)
+        // order on the GPU and decode on the host
+        uint8_t *lk;
+        uint32_t *lm = nullptr;
+        CHECK(hipMalloc(&lk, static_cast<size_t>(rows) * row_bytes));
+        if (meta_words) CHECK(hipMalloc(&lm, static_cast<size_t>(rows) * meta_words * 4));
+        std::vector<uint8_t> hd(static_cast<size_t>(rows) * row_bytes);
+        std::vector<uint32_t> hm(static_cast<size_t>(rows) * meta_words);
+        std::vector<float> kdeq, vdeq;
+        for (int which = 0; which < 2; ++which) {
+          CHECK(kvf_quantize_place(fmt, group, D, which ? dV : dK, B, Hkv, n, 0, 0, nullptr, 0, lk, lm, st));
+          CHECK(hipStreamSynchronize(st));
+          CHECK(hipMemcpy(hd.data(), lk, hd.size(), hipMemcpyDeviceToHost));
+          if (meta_words) CHECK(hipMemcpy(hm.data(), lm, hm.size() * 4, hipMemcpyDeviceToHost));
+          (which ? vdeq : kdeq) = dequantise(fmt, group, D, rows, hd, hm);
+        }
+        CHECK(hipFree(lk));
+        if (lm) CHECK(hipFree(lm));
+        ref = attention(B, H, Hkv, D, n, q, kdeq, vdeq, scale, threads);
+        cur_fmt = fkey;
+      }
+
+      DeviceCache c;
+      long long rows_alloc = rows;
+      std::vector<int32_t> table;
+      if (paged) {
+        c.max_blocks = (n + bt - 1) / bt;
+        const long long pages = 1LL * B * c.max_blocks;
+        table.resize(static_cast<size_t>(pages));
+        kvfh_page_table(pages, seed + 17, table.data());
+        rows_alloc = pages * Hkv * bt;
+        CHECK(hipMalloc(&c.table, table.size() * 4));
+        CHECK(hipMemcpy(c.table, table.data(), table.size() * 4, hipMemcpyHostToDevice));
+      }
+      CHECK(hipMalloc(&c.k, static_cast<size_t>(rows_alloc) * row_bytes));
+      CHECK(hipMalloc(&c.v, static_cast<size_t>(rows_alloc) * row_bytes));
+      CHECK(hipMemset(c.k, 0, static_cast<size_t>(rows_alloc) * row_bytes));
+      CHECK(hipMemset(c.v, 0, static_cast<size_t>(rows_alloc) * row_bytes));
+      if (meta_words) {
+        CHECK(hipMalloc(&c.km, static_cast<size_t>(rows_alloc) * meta_words * 4));
+        CHECK(hipMalloc(&c.vm, static_cast<size_t>(rows_alloc) * meta_words * 4));
+        CHECK(hipMemset(c.km, 0, static_cast<size_t>(rows_alloc) * meta_words * 4));
+        CHECK(hipMemset(c.vm, 0, static_cast<size_t>(rows_alloc) * meta_words * 4));
+      }
+      CHECK(kvf_quantize_place(fmt, group, D, dK, B, Hkv, n, order, bt, c.table, c.max_blocks, c.k, c.km, st));
+      CHECK(kvf_quantize_place(fmt, group, D, dV, B, Hkv, n, order, bt, c.table, c.max_blocks, c.v, c.vm, st));
+      CHECK(hipStreamSynchronize(st));
+
+      for (size_t idx : members) {
+        const PlanRow &p = plans[idx];
+        const std::string vid = variantOf(p);
+        kvf_args_t a{};
+        a.q = dq;
+        a.k = c.k;
+        a.v = c.v;
+        a.k_meta = reinterpret_cast<const __half2 *>(c.km);
+        a.v_meta = reinterpret_cast<const __half2 *>(c.vm);
+        a.block_table = c.table;
+        a.out = dout;
+        a.part_o = dpo;
+        a.part_ml = dpm;
+        a.B = B;
+        a.H = H;
+        a.Hkv = Hkv;
+        a.n = n;
+        a.splits = p.splits;
+        a.warps = p.warps;
+        a.group_shift = fmt == 0 ? 0 : static_cast<int>(std::log2(group) + 0.5);
+        a.block_shift = paged ? static_cast<int>(std::log2(bt) + 0.5) : 0;
+        a.max_blocks = c.max_blocks;
+        a.scale_log2 = scale_log2;
+        CHECK(hipMemsetAsync(dout, 0, got.size() * 4, st));
+        hipError_t e = kvf_launch_variant(vid.c_str(), &a, st);
+        if (e == hipSuccess) e = hipStreamSynchronize(st);
+        if (e != hipSuccess) {
+          std::fprintf(stderr, "launch failed (%s) for %s splits=%d warps=%d\n", hipGetErrorString(e), vid.c_str(),
+                       p.splits, p.warps);
+          (void)hipGetLastError();
+          ++skipped;
+          continue;
+        }
+        CHECK(hipMemcpy(got.data(), dout, got.size() * 4, hipMemcpyDeviceToHost));
+        const double err_ref = relL2(got, ref), err_exact = relL2(got, exact);
+        const bool ok = err_ref < 2e-3;
+        if (!ok) ++unverified;
+
+        std::vector<float> ms;
+        for (int r = 0; r < warmup + reps; ++r) {
+          CHECK(hipMemsetAsync(flush, r & 0xff, flush_bytes, st));
+          CHECK(hipEventRecord(e0, st));
+          CHECK(kvf_launch_variant(vid.c_str(), &a, st));
+          CHECK(hipEventRecord(e1, st));
+          CHECK(hipEventSynchronize(e1));
+          float t = 0;
+          CHECK(hipEventElapsedTime(&t, e0, e1));
+          if (r >= warmup) ms.push_back(t * 1000.0f);
+        }
+        std::sort(ms.begin(), ms.end());
+        auto pct = [&](double f) { return ms[std::min(ms.size() - 1, static_cast<size_t>(f * (ms.size() - 1) + 0.5))]; };
+        Stats s;
+        s.median = pct(0.5);
+        s.p25 = pct(0.25);
+        s.p75 = pct(0.75);
+        s.min = ms.front();
+        s.reps = static_cast<int>(ms.size());
+        std::fprintf(out, "%s,%d,%d,%d,%d,%d,%s,%d,%s,%s,%d,%d,%d,%d,%d,%.3f,%.3f,%.3f,%.3f,%d,%.6g,%.6g,%d,%s\n",
+                     p.name.c_str(), p.H, p.Hkv, p.D, p.n, p.batch, p.fmt.c_str(), p.group, p.order.c_str(),
+                     p.residency.c_str(), p.bt, p.splits, p.pack, p.warps, p.unroll, s.median, s.p25, s.p75, s.min,
+                     s.reps, err_exact, err_ref, ok ? 1 : 0, device.c_str());
+        ++done;
+        if (done % 200 == 0) {
+          std::printf("  %lld plans timed (%lld unverified)\n", done, unverified);
+          std::fflush(stdout);
+          std::fflush(out);
+        }
+      }
+      c.release();
+    }
+    for (float *p : {dq, dK, dV, dout, dpo, dpm}) CHECK(hipFree(p));
+    std::fflush(out);
+  }
+  std::fclose(out);
+  CHECK(hipFree(flush));
+  std::printf("\ndone: %lld timed, %lld skipped, %lld failed verification\nwrote %s\n", done, skipped, unverified,
+              out_path.c_str());
+  return unverified ? 3 : 0;
+}

@@ -245,3 +245,20 @@ def test_fused_merge_matches_two_launch(fmt, group, order, bt, G):
         assert int(counters.abs().sum()) == 0
         check(b, fused, f"fused S={splits} w{warps} u{unroll}")
         assert np.max(np.abs(fused - two)) <= 1e-5 * max(1.0, float(np.max(np.abs(two))))
+
+
+@pytest.mark.parametrize("fmt,group", [(R.FMT_F16, 0), (R.FMT_INT8, 64), (R.FMT_INT4, 32)])
+@pytest.mark.parametrize("order", [R.ORD_HEAD, R.ORD_TOKEN])
+@pytest.mark.parametrize("bt", [0, 16])
+@pytest.mark.parametrize("D", [64, 128])
+def test_every_registered_variant(fmt, group, order, bt, D):
+    # every (G, U) of this bucket and head dimension, both wave counts,
+    # split and unsplit: all 192 registered ids run once across the cases
+    ids = set(R.variants())
+    for G in (1, 2, 4, 8):
+        H = 6 if G == 1 else 2 * G
+        b = build(Case(1, H, 2, D, 333, fmt, group, order, bt, seed=11 + G))
+        for i, U in enumerate((2, 4)):
+            assert vid(b, G > 1, U) in ids
+            splits, warps = ((1, 8), (5, 4))[i] if G % 2 == 0 else ((3, 4), (1, 8))[i]
+            check(b, run(b, splits, pack=G > 1, unroll=U, warps=warps), f"G={G} U={U} S={splits} W={warps}")
