@@ -81,6 +81,14 @@ template <int FMT> constexpr int bits_of() {
   return FMT == FMT_F16 ? 16 : FMT == FMT_INT8 ? 8 : 4;
 }
 
+// Bytes of LDS the split kernel's wave combine takes: sO and sM, plus sL for
+// the lo halves of packed hi/lo rows when all three fit in 64 KiB.
+constexpr int LDS_LIMIT = 65536;
+template <int D, int G> constexpr bool hl_lds_fits(int nw) {
+  return (2 * nw * G * D + nw * G * 3) * 4 <= LDS_LIMIT;
+}
+template <int FMT, int D, int GQ, int G> constexpr size_t combine_lds(int nw);
+
 // Tiles kept in flight per wave for the reference's unroll knob U.
 template <int U> constexpr int depth_of() { return U == 2 ? 2 : 3; }
 
@@ -114,6 +122,11 @@ template <int FMT, int D, int GQ, int G> struct Geo {
   static_assert(COLS <= 32, "at most two column passes");
 };
 
+template <int FMT, int D, int GQ, int G> constexpr size_t combine_lds(int nw) {
+  const bool sl = Geo<FMT, D, GQ, G>::HL && hl_lds_fits<D, G>(nw);
+  return (size_t)(nw * G * (sl ? 2 * D + 3 : D + 3)) * sizeof(float);
+}
+
 __device__ __forceinline__ uint32_t perm(uint32_t s0, uint32_t s1, uint32_t sel) {
   return __builtin_amdgcn_perm(s0, s1, sel);
 }
@@ -132,6 +145,23 @@ template <int N> __device__ __forceinline__ float ror16(float x) {
   static_assert(N >= 1 && N <= 15, "rotation");
   return __builtin_bit_cast(
       float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), 0x120 + N, 0xF, 0xF, false));
+}
+
+// Value of lane l ^ 16 and l ^ 32 through gfx950's permlane swaps (VALU, no
+// LDS round trip). permlane16_swap exchanges the odd rows of its first
+// operand with the even rows of its second, permlane32_swap the upper half of
+// the first with the lower half of the second; with x in both, the partner's
+// value sits in the second result for lanes of an even row (resp. the lower
+// half) and in the first result otherwise.
+__device__ __forceinline__ float xor16(float x) {
+  const auto s = __builtin_amdgcn_permlane16_swap(__builtin_bit_cast(uint32_t, x),
+                                                  __builtin_bit_cast(uint32_t, x), false, false);
+  return __builtin_bit_cast(float, (threadIdx.x & 16) ? s[0] : s[1]);
+}
+__device__ __forceinline__ float xor32(float x) {
+  const auto s = __builtin_amdgcn_permlane32_swap(__builtin_bit_cast(uint32_t, x),
+                                                  __builtin_bit_cast(uint32_t, x), false, false);
+  return __builtin_bit_cast(float, (threadIdx.x & 32) ? s[0] : s[1]);
 }
 
 // Sum of x over the columns c' == c (mod G) of the lane's row of 16.
@@ -224,6 +254,7 @@ decode_partial(const Args a, const Ext x, const int final_out) {
   constexpr int CH = Gm::CH, NCH = Gm::NCH, SPC = Gm::SPC, KSTEPS = Gm::KSTEPS;
   constexpr int EV = Gm::EV, VB = Gm::VB, VW = Gm::VW, GRP = Gm::GRP;
   constexpr int DEPTH = depth_of<U>();
+  constexpr bool HL_LDS = HL && hl_lds_fits<D, G>(WPB);
   constexpr int NQ = HL ? 1 : 2;                   // query operands per k-step
   constexpr float UNIT = QUANT ? CODE_SCALE : 1.f; // log2 units per score unit
   constexpr float TAU_S = TAU / UNIT;
@@ -409,8 +440,8 @@ decode_partial(const Args a, const Ext x, const int final_out) {
           sum += v;
         }
       }
-    sum += __shfl_xor(sum, 16);
-    sum += __shfl_xor(sum, 32);
+    sum += xor16(sum);
+    sum += xor32(sum);
     qs[p] = col_lo ? 0.f : sum / UNIT;
   }
 
@@ -545,7 +576,9 @@ decode_partial(const Args a, const Ext x, const int final_out) {
     m_true = fmaxf(m_true, tmax);
     if (__any(tmax > m_run + TAU_S)) { // wave-uniform, rare after the first tile
       float cand = fmaxf(m_run, tmax);
-      for (int mask = G; mask < 64; mask <<= 1) cand = fmaxf(cand, __shfl_xor(cand, mask));
+      for (int mask = G; mask < 16; mask <<= 1) cand = fmaxf(cand, __shfl_xor(cand, mask));
+      cand = fmaxf(cand, xor16(cand));
+      cand = fmaxf(cand, xor32(cand));
       const float alpha =
           cand == -INFINITY ? 1.f : __builtin_amdgcn_exp2f((m_run - cand) * UNIT);
       l_sum *= alpha;
@@ -621,83 +654,118 @@ decode_partial(const Args a, const Ext x, const int final_out) {
   };
 
   // ---- main loop: ring of DEPTH tiles ------------------------------------------
-  for (int kb = 0; kb < nk; kb += DEPTH) {
+  // Steady state: every step issues the real tile DEPTH-1 ahead and consumes
+  // one. The last DEPTH-1 tiles are consumed after the loop without issuing
+  // anything, so no zero-length loads are left in flight at the end of the
+  // stream for the epilogue to wait on.
+  int k = 0;
+  bool streaming = true;
+  while (streaming) {
     static_for<DEPTH>([&](auto Ui) __attribute__((always_inline)) {
       constexpr int u = decltype(Ui)::value;
-      Buf &cur = ring(Ui);
-      const int k = kb + u;
-      issue(ring(std::integral_constant<int, (u + DEPTH - 1) % DEPTH>{}), k + DEPTH - 1);
-      if (k < nk) {
-        const int tbase = (tile_first + wave + nw * k) * TT;
-        if (tbase >= t0 && tbase + TT <= t1) compute(cur, k, std::false_type{});
-        else compute(cur, k, std::true_type{});
+      if (!streaming) return;
+      if (k + DEPTH - 1 >= nk) {
+        streaming = false;
+        return;
       }
+      issue(ring(std::integral_constant<int, (u + DEPTH - 1) % DEPTH>{}), k + DEPTH - 1);
+      const int tbase = (tile_first + wave + nw * k) * TT;
+      if (tbase >= t0 && tbase + TT <= t1) compute(ring(Ui), k, std::false_type{});
+      else compute(ring(Ui), k, std::true_type{});
+      ++k;
+    });
+  }
+  // drain: the tiles still in flight, masked (a full tile computes the same)
+  for (int j = 0; j < DEPTH - 1; ++j, ++k) {
+    if (k >= nk) break;
+    static_for<DEPTH>([&](auto Ui) __attribute__((always_inline)) {
+      if (k % DEPTH == decltype(Ui)::value) compute(ring(Ui), k, std::true_type{});
     });
   }
 
   // ---- wave result: per head (m_run, l, m_true) and O[head][D] ---------------
-  l_sum += __shfl_xor(l_sum, 16);
-  l_sum += __shfl_xor(l_sum, 32);
-  m_true = fmaxf(m_true, __shfl_xor(m_true, 16));
-  m_true = fmaxf(m_true, __shfl_xor(m_true, 32));
+  l_sum += xor16(l_sum);
+  l_sum += xor32(l_sum);
+  m_true = fmaxf(m_true, xor16(m_true));
+  m_true = fmaxf(m_true, xor32(m_true));
   float zrow[PASSES][4];
 #pragma unroll
   for (int p = 0; p < PASSES; ++p) {
     float z = zacc[p];
-    z += __shfl_xor(z, 16);
-    z += __shfl_xor(z, 32);
+    z += xor16(z);
+    z += xor32(z);
 #pragma unroll
     for (int i = 0; i < 4; ++i) zrow[p][i] = __shfl(z, 16 * r + ((4 * r + i) & 15));
   }
-  if constexpr (HL) {
-    // rows 8-15 (lane-rows 2, 3) hold the lo halves of rows 0-7
-#pragma unroll
-    for (int e = 0; e < EV; ++e)
-#pragma unroll
-      for (int i = 0; i < 4; ++i) acc[0][e][i] += __shfl_xor(acc[0][e][i], 32);
-  }
 
   extern __shared__ float smem[];
-  // layout: sO[nw][G][D], then sM[nw][G][3]
+  // layout: sO[nw][G][D], sM[nw][G][3], then (HL_LDS) sL[nw][G][D]
   float *sO = smem;
   float *sM = smem + nw * G * D;
+  float *sL = sM + nw * G * 3;
   if (r == 0 && c < G) {
     sM[(wave * G + c) * 3 + 0] = m_run * UNIT;
     sM[(wave * G + c) * 3 + 1] = l_sum;
     sM[(wave * G + c) * 3 + 2] = m_true * UNIT;
   }
   const int gdim = (c * EV) / GRP; // group of this lane's V dims
+  // With HL, accumulator rows 8-15 (lane-rows 2 and 3) hold the lo halves of
+  // rows 0-7: they are stored to their own LDS rows (sL) and the combine adds
+  // them, which keeps the cross-half sum off the VALU (the zero-point sum
+  // enters once, with the hi half). Where sL would not fit beside sO, the
+  // halves are summed with a lane swap instead.
+  if constexpr (HL && !HL_LDS) {
+#pragma unroll
+    for (int e = 0; e < EV; ++e)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) acc[0][e][i] += xor32(acc[0][e][i]);
+  }
 #pragma unroll
   for (int p = 0; p < PASSES; ++p)
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      const int row = p * 16 + 4 * r + i; // (group, head) pair of accumulator row
-      const bool canon = HL ? row < COLS : (PASSES > 1 || row < COLS);
-      if (canon && (row % COLS) / G == gdim) {
-        const int hh = row % G;
+      const int row = p * 16 + 4 * r + i; // accumulator row
+      const bool lo_half = HL && row >= 8;
+      const int pr = HL ? (row & 7) : row; // its (group, head) pair
+      const bool canon = HL ? (HL_LDS || !lo_half) && pr < COLS : (PASSES > 1 || pr < COLS);
+      if (canon && (pr % COLS) / G == gdim) {
+        float *dst = (lo_half ? sL : sO) + (wave * G + pr % G) * D + c * EV;
 #pragma unroll
-        for (int e = 0; e < EV; ++e) {
-          const float o = QUANT ? fmaf(acc[p][e][i], CODE_SCALE, zrow[p][i]) : acc[p][e][i];
-          sO[(wave * G + hh) * D + c * EV + e] = o;
-        }
+        for (int e = 0; e < EV; ++e)
+          dst[e] = QUANT ? fmaf(acc[p][e][i], CODE_SCALE, lo_half ? 0.f : zrow[p][i]) : acc[p][e][i];
       }
     }
   __syncthreads();
 
+  // every LDS read of an output element is issued before any is used: the
+  // waves' (m_run, l, m_true) and partial outputs, then a branch-free
+  // log-sum-exp over the waves (a wave with m_run = -inf saw no token and
+  // contributes nothing; all -inf leaves L = O = 0)
   const int nthreads = nw * 64;
-  for (int idx = threadIdx.x; idx < G * D; idx += nthreads) {
+#pragma unroll
+  for (int idx0 = 0; idx0 < G * D; idx0 += nthreads) {
+    const int idx = idx0 + threadIdx.x;
+    if (G * D % nthreads != 0 && idx >= G * D) break;
     const int hh = idx / D, col = idx % D;
+    float mr[nw], lw[nw], mt[nw], ov[nw];
+#pragma unroll
+    for (int w2 = 0; w2 < nw; ++w2) {
+      mr[w2] = sM[(w2 * G + hh) * 3 + 0];
+      lw[w2] = sM[(w2 * G + hh) * 3 + 1];
+      mt[w2] = sM[(w2 * G + hh) * 3 + 2];
+      ov[w2] = sO[(w2 * G + hh) * D + col];
+      if constexpr (HL_LDS) ov[w2] += sL[(w2 * G + hh) * D + col];
+    }
     float M = -INFINITY;
-    for (int w2 = 0; w2 < nw; ++w2) M = fmaxf(M, sM[(w2 * G + hh) * 3 + 2]);
+#pragma unroll
+    for (int w2 = 0; w2 < nw; ++w2) M = fmaxf(M, mt[w2]);
     float L = 0.f, O = 0.f;
-    if (M != -INFINITY) {
-      for (int w2 = 0; w2 < nw; ++w2) {
-        const float mr = sM[(w2 * G + hh) * 3 + 0];
-        if (mr == -INFINITY) continue;
-        const float wgt = __builtin_amdgcn_exp2f(mr - M);
-        L = fmaf(sM[(w2 * G + hh) * 3 + 1], wgt, L);
-        O = fmaf(sO[(w2 * G + hh) * D + col], wgt, O);
-      }
+#pragma unroll
+    for (int w2 = 0; w2 < nw; ++w2) {
+      const bool live = M != -INFINITY && mr[w2] != -INFINITY;
+      const float wgt = live ? __builtin_amdgcn_exp2f(mr[w2] - M) : 0.f;
+      L = live ? fmaf(lw[w2], wgt, L) : L;
+      O = live ? fmaf(ov[w2], wgt, O) : O;
     }
     const int hq = G > 1 ? hkv * G + hh : hb;
     const long long head = (long long)b * a.H + hq;
@@ -825,7 +893,7 @@ hipError_t launch_group(const Args &a, const Ext &x, const Launch &l, hipStream_
   const bool fused = x.counters && !final_out && !l.partial_only;
   Ext xk = x;
   if (!fused) xk.counters = nullptr;
-  size_t lds = (size_t)a.warps * G * (D + 3) * sizeof(float);
+  size_t lds = combine_lds<FMT, D, GQ, G>(a.warps);
   if (fused) lds = std::max(lds, (size_t)(a.splits + a.warps * 64) * sizeof(float));
   auto kernel = a.warps == 4 ? &decode_partial<FMT, D, GQ, G, U, ORD, PAGED, 4>
                              : &decode_partial<FMT, D, GQ, G, U, ORD, PAGED, 8>;
