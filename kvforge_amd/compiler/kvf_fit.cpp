@@ -68,6 +68,7 @@ double kendall(const std::vector<double> &a, const std::vector<double> &b) {
 }
 
 bool eligible(const SweepRow &r, const Calib &c, const Eligibility &e) {
+  if (!e.keys.empty() && std::find(e.keys.begin(), e.keys.end(), r.plan.fmt.key()) == e.keys.end()) return false;
   if (!e.formats.empty() &&
       std::find(e.formats.begin(), e.formats.end(), std::string(formatName(r.plan.fmt.fmt))) == e.formats.end())
     return false;
@@ -227,7 +228,7 @@ Calib calibrate(const std::vector<SweepRow> &rows, const Machine &m, const Calib
     double lo, hi;
     bool log;
   };
-  const Knob knobs[] = {
+  std::vector<Knob> knobs = {
       {&Calib::r0_bytes, 2.0, 8192.0, true},     {&Calib::c_page_ns, 0.5, 4000.0, true},
       {&Calib::unpack_l2_hit, 0.0, 1.0, false},  {&Calib::issue_eff, 0.02, 1.0, true},
       {&Calib::meta_waste, 0.0, 2.0, false},     {&Calib::overlap_p, 1.0, 24.0, true},
@@ -235,6 +236,12 @@ Calib calibrate(const std::vector<SweepRow> &rows, const Machine &m, const Calib
       {&Calib::lat_scale, 1.0, 40.0, true},      {&Calib::warp_w0, 0.5, 40.0, true},
   };
   Calib best = start;
+  if (m.cdna()) {
+    // the CDNA form's own constants (per-CU stream rate, spill cost)
+    knobs.push_back({&Calib::cu_frac, 0.1, 1.5, false});
+    knobs.push_back({&Calib::spill_cost, 0.0, 4.0, false});
+    best.cdna = true;
+  }
   double best_loss = loss(best);
   for (int round = 0; round < 6; ++round) {
     const double span = round == 0 ? 1.0 : std::pow(0.5, round);
@@ -284,18 +291,15 @@ std::vector<std::string> heldOutShapes(const std::vector<SweepRow> &rows, int ev
   return held;
 }
 
-std::string evaluationReport(const std::vector<SweepRow> &rows, const Machine &m, const Calib &c,
-                             const ShapeFilter &use) {
-  struct Class {
-    const char *title;
-    Eligibility e;
-  };
-  std::vector<Class> classes(3);
-  classes[0].title = "lossless only (f16)";
-  classes[0].e.formats = {"f16"};
-  classes[1].title = "accuracy limit 0.02 (f16 + int8)";
-  classes[1].e.max_rel_err = 0.02;
-  classes[2].title = "no accuracy limit (f16 + int8 + int4)";
+namespace {
+
+struct Class {
+  std::string title;
+  Eligibility e;
+};
+
+std::string report(const std::vector<SweepRow> &rows, const Machine &m, const Calib &c, const ShapeFilter &use,
+                   const std::vector<Class> &classes) {
   std::ostringstream o;
   for (const auto &cl : classes) {
     const Metrics mt = evaluateSweep(rows, m, c, cl.e, use);
@@ -311,6 +315,28 @@ std::string evaluationReport(const std::vector<SweepRow> &rows, const Machine &m
     o << std::setprecision(6) << mt.per_shape << "\n";
   }
   return o.str();
+}
+
+} // namespace
+
+std::string evaluationReport(const std::vector<SweepRow> &rows, const Machine &m, const Calib &c,
+                             const ShapeFilter &use) {
+  std::vector<Class> classes(3);
+  classes[0].title = "lossless only (f16)";
+  classes[0].e.formats = {"f16"};
+  classes[1].title = "accuracy limit 0.02 (f16 + int8)";
+  classes[1].e.max_rel_err = 0.02;
+  classes[2].title = "no accuracy limit (f16 + int8 + int4)";
+  return report(rows, m, c, use, classes);
+}
+
+std::string evaluationReport(const std::vector<SweepRow> &rows, const Machine &m, const Calib &c,
+                             const ShapeFilter &use, const std::vector<std::string> &keys) {
+  std::vector<Class> classes(1);
+  for (const auto &k : keys) classes[0].title += (classes[0].title.empty() ? "" : " + ") + k;
+  classes[0].title = "format " + classes[0].title + " only";
+  classes[0].e.keys = keys;
+  return report(rows, m, c, use, classes);
 }
 
 } // namespace kvfc

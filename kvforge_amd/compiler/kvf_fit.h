@@ -40,6 +40,7 @@ struct Metrics {
 struct Eligibility {
   double max_rel_err = 0;           // 0: every format
   std::vector<std::string> formats; // empty: every format
+  std::vector<std::string> keys;    // empty: every group; else exact keys ("int8_64")
 };
 
 using ShapeFilter = std::function<bool(const std::string &)>;
@@ -54,5 +55,8 @@ std::vector<std::string> heldOutShapes(const std::vector<SweepRow> &rows, int ev
 // The three eligibility classes a user can ask for, scored and printed.
 std::string evaluationReport(const std::vector<SweepRow> &rows, const Machine &m, const Calib &c,
                              const ShapeFilter &use);
+// One class: the plans of the listed format keys only (e.g. {"int8_64"}).
+std::string evaluationReport(const std::vector<SweepRow> &rows, const Machine &m, const Calib &c,
+                             const ShapeFilter &use, const std::vector<std::string> &keys);
 
 } // namespace kvfc

@@ -5,6 +5,7 @@
 #include "kvf_front.h"
 
 #include <filesystem>
+#include <algorithm>
 #include <fstream>
 #include <iomanip>
 #include <iostream>
@@ -44,7 +45,7 @@ int usage() {
                "  kvf calibrate --sweep A.csv[,B.csv] --machine FILE [--out FILE] [--holdout-every N]\n"
                "  kvf predict   --sweep A.csv --machine FILE [--calib FILE] [--out FILE]\n"
                "  kvf evaluate  --sweep A.csv[,B.csv] --machine FILE [--calib FILE]\n"
-               "                [--holdout-every N] [--which fit|heldout|all]\n\n"
+               "                [--holdout-every N] [--which fit|heldout|all] [--only int8:64,...]\n\n"
                "  --quant        search lossy formats (int8, int4) too\n"
                "  --max-err X    accuracy limit for lossy formats (implies --quant)\n"
                "  --machine FILE machine description (overrides `target machine`)\n"
@@ -190,9 +191,22 @@ int run(const Cli &c) {
     }
     const Calib k = c.has("calib") ? loadCalib(c.opt("calib")) : Calib::defaults();
     const std::string which = c.opt("which", "all");
+    const ShapeFilter &pick = which == "fit" ? fitted : which == "heldout" ? heldout : every;
     std::cout << "machine " << m.name << ", constants " << (c.has("calib") ? c.opt("calib") : "defaults")
-              << ", shapes: " << which << "\n\n"
-              << evaluationReport(rows, m, k, which == "fit" ? fitted : which == "heldout" ? heldout : every);
+              << ", shapes: " << which << "\n\n";
+    if (c.has("only")) {
+      // e.g. --only int8:64,int8:128 : the plans of those formats alone
+      std::vector<std::string> keys;
+      std::stringstream ss(c.opt("only"));
+      std::string f;
+      while (std::getline(ss, f, ',')) {
+        std::replace(f.begin(), f.end(), ':', '_');
+        keys.push_back(f);
+      }
+      std::cout << evaluationReport(rows, m, k, pick, keys);
+    } else {
+      std::cout << evaluationReport(rows, m, k, pick);
+    }
     return 0;
   }
   if (c.positional.empty()) return usage();

@@ -283,6 +283,20 @@ Machine loadMachine(const std::filesystem::path &p) {
     if (!rin) throw std::runtime_error("cannot read resource table " + rp.string());
     std::string rl;
     std::getline(rin, rl); // header
+    if (rl.find("waves") != std::string::npos) {
+      // gfx950 layout: fmt,d,group,g,u,ord,paged,waves,vgpr,agpr,sgpr,scratch,occupancy
+      while (std::getline(rin, rl)) {
+        std::vector<int> f;
+        std::stringstream ss(rl);
+        std::string tok;
+        while (std::getline(ss, tok, ',')) f.push_back(std::stoi(tok));
+        if (f.size() < 13) continue;
+        std::string key;
+        for (int i = 0; i < 8; ++i) key += (i ? "_" : "") + std::to_string(f[i]);
+        m.kernel_res[key] = Machine::KernelRes{f[8], f[9], f[11], f[12]};
+      }
+      return m;
+    }
     while (std::getline(rin, rl)) {
       std::vector<int> f;
       std::stringstream ss(rl);
@@ -367,8 +381,14 @@ Calib loadCalib(const std::filesystem::path &p) {
   Calib c = Calib::defaults();
   readKeyValues(p, "calibration file", " \t\r\n", [&](const std::string &k, const std::string &raw) {
     const double v = std::stod(raw);
-    if (k.rfind("rel_err.", 0) == 0) c.rel_err[k.substr(8)] = v;
-    else calibScalar(c, k) = v;
+    if (k.rfind("rel_err.", 0) == 0) {
+      c.rel_err[k.substr(8)] = v;
+    } else if (k == "cu_frac" || k == "spill_cost") {
+      (k == "cu_frac" ? c.cu_frac : c.spill_cost) = v;
+      c.cdna = true;
+    } else {
+      calibScalar(c, k) = v;
+    }
   });
   return c;
 }
@@ -378,6 +398,7 @@ std::string dumpCalib(const Calib &c) {
   o << std::setprecision(8);
   Calib t = c;
   for (const char *k : calibScalarKeys()) o << k << " = " << calibScalar(t, k) << "\n";
+  if (c.cdna) o << "cu_frac = " << c.cu_frac << "\nspill_cost = " << c.spill_cost << "\n";
   for (const auto &kv : c.rel_err) o << "rel_err." << kv.first << " = " << kv.second << "\n";
   return o.str();
 }
@@ -568,63 +589,73 @@ Cost warpEvaluate(const DecodeSpec &s, const Machine &m, const Calib &c, const P
 }
 
 // ------------------------------------------------------------ CDNA (wave64)
-// Geometry of the gfx950 split kernel (kvforge_amd/csrc/kvf_kernels.hpp):
-// a wavefront consumes 32-token tiles, keeps depth(U) - 1 tiles in flight
-// ahead of the one it computes, and per tile issues the MFMAs and VALU
-// operations counted below.
+// The gfx950 split kernel (kvforge_amd/csrc/kvf_kernels.hpp) works in
+// 32-token tiles: a wave keeps depth(U) - 1 tiles in flight ahead of the one
+// it computes, tiles are dealt round-robin to the W waves of a workgroup, and
+// one workgroup covers one (split, KV head or query head, sequence). Terms:
+//
+//   residency  workgroups per CU = min(blocks per CU, waves/SIMD * 4 / W) from
+//              the compiler's occupancy for that instantiation (resource
+//              table), else from a register estimate; blocks beyond
+//              CUs x residency run in further rounds
+//   stream     per workgroup min(cu_frac * bw_sm / workgroups on its CU,
+//              bytes in flight / (lat * lat_scale)) (Little's law), the device
+//              capped at bw_peak * eta (run-length efficiency)
+//   fill       bytes in flight at the start, drained at peak bandwidth before
+//              the stream is steady: deeper rings and more waves cost queueing
+//   GQA        unpacked query heads re-read their KV head; the re-reads hit L2
+//              with probability unpack_l2_hit * window and go at bw_l2, the
+//              rest come from HBM again
+//   issue      VALU wave-instructions per tile (MFMA cycles / 4 folded in) at
+//              one wave-instruction per SIMD slot, waves per SIMD sharing it,
+//              spills (scratch bytes per lane) costing spill_cost per 64 B
+//   fixed      launch_frac and merge_frac (second kernel) of launch_us, plus
+//              warp_w0 loaded latencies per round of workgroups (query load,
+//              first tile, wave combine and partial write)
+//   paging     c_page_ns per page a workgroup walks, per round
 struct CdnaTile {
-  int depth = 2;           // ring of tiles per wave
-  double bytes = 0;        // K + V + meta bytes of one tile
-  double valu = 0;         // VALU instructions per tile per wave
-  double mfma_cycles = 0;  // matrix-core cycles per tile per wave
+  int depth = 2;     // ring of tiles per wave
+  double bytes = 0;  // K + V + meta bytes of one tile
+  double instr = 0;  // wave-instructions per tile (VALU + MFMA cycles / 4)
 };
 
 CdnaTile cdnaTile(const DecodeSpec &s, const Plan &p, int G) {
   CdnaTile t;
   t.depth = p.part.unroll == 2 ? 2 : 3;
-  const double data_row = p.fmt.dataRowBytes(s.d);
-  const double meta_row = p.fmt.metaRowBytes(s.d);
-  t.bytes = 32.0 * 2.0 * (data_row + meta_row);
+  t.bytes = 32.0 * 2.0 * (p.fmt.dataRowBytes(s.d) + p.fmt.metaRowBytes(s.d));
   const int ng = p.fmt.isQuantized() ? s.d / p.fmt.group : 1;
   const int cols = G * ng;
-  const bool hl = cols <= 8;                   // hi/lo share one MFMA
+  const bool hl = cols <= 8; // hi/lo share one MFMA
   const int passes = cols > 16 ? 2 : 1;
   const int nq = hl ? 1 : 2;
-  const int ksteps = s.d / 32;
-  const int ev = s.d / 16;
-  // QK: 2 sub-tiles x k-steps x (hi, lo) x passes; PV: one per 16 dims
-  const double mfma = 2.0 * ksteps * nq * passes + 1.0 * ev * nq * passes;
-  t.mfma_cycles = 16.0 * mfma; // 16x16x32 binary16: 16 cycles each
-  const double elems = 32.0 * s.d;       // per tile, K and V each
+  // QK: 2 sub-tiles x D/32 k-steps x (hi, lo) x passes; PV: D/16 per (hi, lo, pass)
+  const double mfma = 2.0 * (s.d / 32) * nq * passes + 1.0 * (s.d / 16) * nq * passes;
+  // code -> binary16 conversions per element of K and V, softmax per token slot
   const double k_conv = p.fmt.fmt == Format::F16 ? 0.0 : p.fmt.fmt == Format::INT8 ? 0.5 : 0.875;
   const double v_conv = p.fmt.fmt == Format::INT4 ? 0.8 : 0.5;
-  // scores and softmax per lane: 8 tokens, plus meta broadcasts for
-  // quantized formats; the rest is per-lane constant work
-  const double per_lane_tokens = 8.0;
-  const double softmax = per_lane_tokens * (p.fmt.isQuantized() ? 9.0 : 6.0) * passes;
-  t.valu = (k_conv + v_conv) * elems / 64.0 + softmax + 24.0;
+  const double softmax = 8.0 * (p.fmt.isQuantized() ? 9.0 : 6.0) * passes;
+  t.instr = (k_conv + v_conv) * 32.0 * s.d / 64.0 + softmax + 24.0 + 16.0 * mfma / 4.0;
   return t;
 }
 
-// Waves a SIMD holds for a kernel of `regs` registers per lane (512-entry
-// unified VGPR/AGPR file per lane, allocation granule 8).
-int wavesPerSimd(int regs) {
-  const int r = std::max(8, (regs + 7) / 8 * 8);
-  return std::max(1, std::min(8, 512 / r));
+std::string cdnaKernelKey(const DecodeSpec &s, const Plan &p, int G) {
+  const int fmt = p.fmt.fmt == Format::F16 ? 0 : p.fmt.fmt == Format::INT8 ? 1 : 2;
+  const int group = p.fmt.isQuantized() ? p.fmt.group : 0;
+  return std::to_string(fmt) + "_" + std::to_string(s.d) + "_" + std::to_string(group) + "_" + std::to_string(G) +
+         "_" + std::to_string(p.part.unroll) + "_" + std::to_string(p.layout.order == Order::HeadMajor ? 0 : 1) +
+         "_" + std::to_string(p.layout.paged() ? 1 : 0) + "_" + std::to_string(p.part.warps);
 }
 
-int cdnaKernelRegs(const Machine &m, const DecodeSpec &s, const Plan &p, int G) {
-  const int fmt = p.fmt.fmt == Format::F16 ? 0 : p.fmt.fmt == Format::INT8 ? 1 : 2;
-  const int ord = p.layout.order == Order::HeadMajor ? 0 : 1;
-  const std::string key = std::to_string(fmt) + "_" + std::to_string(s.d) + "_" + std::to_string(G) + "_" +
-                          std::to_string(p.part.unroll) + "_" + std::to_string(ord) + "_" +
-                          std::to_string(p.layout.paged() ? 1 : 0) + "_" + std::to_string(p.part.warps);
-  const int r = m.regsFor(key);
-  if (r > 0) return r;
-  // estimate: ring buffers + query operands + accumulators
-  const CdnaTile t = cdnaTile(s, p, G);
-  const double per_tile_regs = t.bytes / 64.0 / 4.0;
-  return static_cast<int>(std::min(512.0, 96.0 + per_tile_regs * t.depth));
+Machine::KernelRes cdnaResources(const Machine &m, const DecodeSpec &s, const Plan &p, int G, const CdnaTile &t) {
+  const auto it = m.kernel_res.find(cdnaKernelKey(s, p, G));
+  if (it != m.kernel_res.end()) return it->second;
+  // estimate: query operands, accumulators and the ring in VGPRs; 512
+  // registers per lane and SIMD, granule 8
+  Machine::KernelRes r;
+  r.vgpr = static_cast<int>(std::min(512.0, 96.0 + t.bytes / 64.0 / 4.0 * t.depth));
+  const int alloc = (r.vgpr + 7) / 8 * 8;
+  r.occupancy = std::max(1, std::min(8, 512 / alloc));
+  return r;
 }
 
 Cost cdnaEvaluate(const DecodeSpec &s, const Machine &m, const Calib &c, const Plan &p,
@@ -635,75 +666,60 @@ Cost cdnaEvaluate(const DecodeSpec &s, const Machine &m, const Calib &c, const P
   const int G = pack ? g : 1;
   const int loading_heads = pack ? s.H_kv : s.H;
   const int waves = p.part.warps;
-  const int simds = 4;
-
-  // workgroups a CU holds: wave slots, registers (a workgroup spreads its
-  // waves over the 4 SIMDs) and LDS (the wave combine)
-  const int regs = cdnaKernelRegs(m, s, p, G);
-  const int wg_per_cu_regs = std::max(1, wavesPerSimd(regs) * simds / waves);
-  const double lds = 1.0 * waves * G * (s.d + 3) * 4.0;
-  const int wg_per_cu_lds = std::max(1, static_cast<int>((160.0 * 1024.0) / lds));
-  int resident_cap = std::min({m.max_blocks_per_sm, m.max_warps_per_sm / waves, wg_per_cu_regs, wg_per_cu_lds});
-  resident_cap = std::max(1, resident_cap);
-  const double resident_total = 1.0 * m.sms * resident_cap;
-
-  // unpacked GQA: the g workgroups of a KV head share its rows through L2
-  // only while they are resident together
-  const double window = std::clamp(resident_total / (1.0 * g * p.part.splits), 0.0, 1.0);
-  const double reread = pack ? 1.0 : 1.0 + (g - 1) * (1.0 - c.unpack_l2_hit * window);
-  double main_bytes = 0;
-  countBytes(k, s, m, c, p, reread, main_bytes);
-
-  k.blocks = 1LL * p.part.splits * loading_heads * s.batch;
-  k.active_sms = static_cast<int>(std::min<long long>(k.blocks, m.sms));
-  const long long per_sm = (k.blocks + m.sms - 1) / m.sms;
-  k.resident_blocks = static_cast<int>(std::clamp<long long>(per_sm, 1, resident_cap));
-
-  // Little's law: each wave keeps depth-1 tiles of K, V and meta in flight
   const CdnaTile t = cdnaTile(s, p, G);
-  const double bif_block = 1.0 * waves * (t.depth - 1) * t.bytes;
-  k.bif_sm_bytes = k.resident_blocks * bif_block;
+  const Machine::KernelRes kr = cdnaResources(m, s, p, G, t);
+
+  // residency and rounds
+  const int resident_cap =
+      std::max(1, std::min({m.max_blocks_per_sm, m.max_warps_per_sm / waves, kr.occupancy * 4 / waves}));
+  const long long capacity = 1LL * m.sms * resident_cap;
+  k.blocks = 1LL * p.part.splits * loading_heads * s.batch;
+  const long long conc = std::min(k.blocks, capacity);
+  const long long rounds = (k.blocks + capacity - 1) / capacity;
+  const long long per_cu = (conc + m.sms - 1) / m.sms;
+  k.active_sms = static_cast<int>(std::min<long long>(conc, m.sms));
+  k.resident_blocks = static_cast<int>(per_cu);
+  k.imbalance = static_cast<double>(rounds * capacity) / static_cast<double>(k.blocks);
+
+  // unpacked GQA: the g query heads of a KV head share its rows through L2
+  // while they are resident together
+  const double window = std::clamp(static_cast<double>(capacity) / (1.0 * g * p.part.splits), 0.0, 1.0);
+  const double hit = pack ? 0.0 : c.unpack_l2_hit * window;
+  const double reread_hbm = pack ? 1.0 : 1.0 + (g - 1) * (1.0 - hit);
+  double main_bytes = 0;
+  countBytes(k, s, m, c, p, reread_hbm, main_bytes);
 
   const double chunk = std::ceil(static_cast<double>(s.n) / p.part.splits);
   k.eta = runEfficiency(runBytes(s, p.fmt, p.layout, chunk), c.r0_bytes);
-  const long long capacity = static_cast<long long>(resident_total);
-  auto aggregate = [&](long long nb) {
-    const long long act = std::min<long long>(nb, m.sms);
-    const long long per = std::clamp<long long>((nb + m.sms - 1) / m.sms, 1, resident_cap);
-    return k.eta * m.bwDeviceGbs(static_cast<int>(act), per * bif_block, c.lat_scale);
-  };
-  memoryTime(k, c, capacity, m.sms, per_sm, main_bytes, aggregate);
+  const double lat_us = m.lat_ns * std::max(1.0, c.lat_scale) / 1000.0;
 
-  // issue time: VALU wave-instructions plus matrix-core cycles of every
-  // tile, over the SIMDs of the active CUs; a wave64 FP32 FMA instruction
-  // is 128 FLOPs, so f32 GFLOP/s over 128 is wave-instructions per ns
-  {
-    const double tiles_per_block = std::ceil(chunk / 32.0);
-    const double tiles = tiles_per_block * k.blocks;
-    const double wave_instr_rate = m.fSmGflops() / 128.0; // per CU, per ns
-    const double clock_ghz = wave_instr_rate / simds * 4.0; // one VALU op per 4 cycles per SIMD
-    const double instr = tiles * (t.valu + t.mfma_cycles / 4.0);
-    const double waves_per_cu = 1.0 * k.resident_blocks * waves;
-    const double occupancy = 1.0 - std::exp(-waves_per_cu / c.warp_w0);
-    (void)clock_ghz;
-    k.t_cmp_us = instr / (std::max(1, k.active_sms) * wave_instr_rate * c.issue_eff * occupancy) / 1000.0;
-  }
+  // stream: bytes per workgroup from HBM and (re-reads) from L2
+  const double wg_kv = (k.kv_bytes + k.meta_bytes) / static_cast<double>(k.blocks);
+  const double wg_l2 = pack ? 0.0 : wg_kv / reread_hbm * (g - 1) * hit;
+  const double bif_wg = 1.0 * waves * (t.depth - 1) * t.bytes;
+  k.bif_sm_bytes = per_cu * bif_wg;
+  const double r_wg = std::min(c.cu_frac * m.bw_sm_gbs / per_cu, bif_wg / 1000.0 / lat_us); // GB/s
+  const double peak = m.bw_peak_gbs * k.eta;
+  k.bw_eff_gbs = std::min(peak, conc * r_wg);
+  const double l2 = m.bw_l2_gbs > 0 ? m.bw_l2_gbs : m.bw_peak_gbs;
+  k.t_mem_us = rounds * (conc * wg_kv / (k.bw_eff_gbs * 1000.0) + conc * wg_l2 / (l2 * 1000.0));
+
+  // issue: tiles per wave, waves per SIMD sharing its slots
+  const double tiles_wave = std::ceil((std::ceil(chunk / 32.0) + 1.0) / waves);
+  const double simd_waves = std::max(1.0, waves * per_cu / 4.0);
+  const double simd_rate = m.fSmGflops() / 4.0 / 128.0; // wave-instructions per ns per SIMD
+  k.t_cmp_us = rounds * tiles_wave * t.instr * simd_waves * (1.0 + c.spill_cost * kr.scratch / 64.0) /
+               (simd_rate * std::max(1e-6, c.issue_eff)) / 1000.0;
   k.memory_bound = k.t_mem_us >= k.t_cmp_us;
   const double t_par =
       std::pow(std::pow(k.t_mem_us, c.overlap_p) + std::pow(k.t_cmp_us, c.overlap_p), 1.0 / c.overlap_p);
 
-  // a second kernel: launch floor plus every partial read back
-  const double floor_us = m.kernel_floor_us > 0 ? m.kernel_floor_us : m.launch_us;
-  if (p.part.splits > 1) k.t_merge_us = c.merge_frac * floor_us + k.partial_bytes / (m.bw_l2_gbs * 1000.0);
-  // paged: page ids are fetched a batch of 32 tiles at a time, one dependent
-  // round trip per batch and wave
-  if (p.layout.paged() && p.layout.block_tokens > 0) {
-    const double batches = std::ceil(std::ceil(chunk / 32.0) / (32.0 * waves)) * k.blocks * waves;
-    const double pages = std::ceil(chunk / p.layout.block_tokens) * k.blocks;
-    const double parallel = std::max(1.0, 1.0 * k.active_sms * k.resident_blocks * waves);
-    k.t_page_us = (batches * m.lat_ns + pages * c.c_page_ns) / parallel / 1000.0;
-  }
-  k.t_launch_us = c.launch_frac * floor_us;
+  // fill: the bytes requested at the start queue at peak bandwidth
+  const double t_fill = conc * bif_wg / (peak * 1000.0);
+  if (p.part.splits > 1) k.t_merge_us = c.merge_frac * m.launch_us + k.partial_bytes / (l2 * 1000.0);
+  if (p.layout.paged() && p.layout.block_tokens > 0)
+    k.t_page_us = rounds * std::ceil(chunk / p.layout.block_tokens) * c.c_page_ns / 1000.0;
+  k.t_launch_us = c.launch_frac * m.launch_us + c.warp_w0 * lat_us * rounds + t_fill;
   k.t_total_us = t_par + k.t_merge_us + k.t_page_us + k.t_launch_us;
   k.achieved_gbs = k.t_total_us > 0 ? (k.kv_bytes + k.meta_bytes) / (k.t_total_us * 1000.0) : 0;
   k.frac_of_peak = m.bw_peak_gbs > 0 ? k.achieved_gbs / m.bw_peak_gbs : 0;

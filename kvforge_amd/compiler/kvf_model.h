@@ -124,6 +124,13 @@ struct Machine {
   int regs_per_sm = 0;
   std::string resources_file;
   std::map<std::string, int> kernel_regs;
+  // gfx950 resource table (machines/resources_gfx950.csv, written by
+  // kvforge_amd/tools/dump_resources.py): per split-kernel instantiation,
+  // keyed "fmt_d_group_g_u_ord_paged_waves".
+  struct KernelRes {
+    int vgpr = 0, agpr = 0, scratch = 0, occupancy = 0;
+  };
+  std::map<std::string, KernelRes> kernel_res;
   // CDNA keys (written by kvforge_amd/tools/bw_probe); wave_size = 64 selects
   // the CDNA form of the cost model.
   int wave_size = 32;
@@ -162,6 +169,13 @@ struct Calib {
   double launch_frac = 0.5;
   double merge_frac = 0.3;
   double meta_waste = 1.0;
+  // CDNA form only: per-CU stream rate of the split kernel as a fraction of
+  // the machine's bw_sm_gbs, and the issue cost of register spills. They are
+  // written to and read from calibration files only when `cdna` is set, so a
+  // file for a 32-lane-warp machine keeps the reference's keys exactly.
+  double cu_frac = 0.6;
+  double spill_cost = 0.5;
+  bool cdna = false;
   std::map<std::string, double> rel_err;
   static Calib defaults();
 };
