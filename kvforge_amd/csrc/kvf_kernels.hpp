@@ -244,6 +244,8 @@ __device__ __forceinline__ int tau(int r, int i) { return (i >> 2) * SUB + 4 * r
 
 template <int D, int NT>
 __device__ void merge_head(const Args &a, const Ext &x, long long head, float *lds);
+template <int D, int G, int NT>
+__device__ void merge_group(const Args &a, const Ext &x, long long head0, float *lds);
 
 template <int FMT, int D, int GQ, int G, int U, int ORD, bool PAGED, int WPB>
 __global__ void __launch_bounds__(WPB * 64)
@@ -774,31 +776,124 @@ decode_partial(const Args a, const Ext x, const int final_out) {
       if (x.out16) x.out16[head * D + col] = (_Float16)res;
       else a.out[head * D + col] = res;
     } else {
-      a.part_o[(head * a.splits + split) * D + col] = O;
-      if (col == 0) {
-        a.part_ml[(head * a.splits + split) * 2] = M;
-        a.part_ml[(head * a.splits + split) * 2 + 1] = L;
+      // fused step: agent-scope atomic stores (write-through to the level
+      // every XCD sees), published below without an L2 writeback
+      float *po = a.part_o + (head * a.splits + split) * D + col;
+      float *pm = a.part_ml + (head * a.splits + split) * 2;
+      if (x.counters) {
+        __hip_atomic_store(po, O, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (col == 0) {
+          __hip_atomic_store(pm, M, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+          __hip_atomic_store(pm + 1, L, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+      } else {
+        *po = O;
+        if (col == 0) {
+          pm[0] = M;
+          pm[1] = L;
+        }
       }
     }
   }
 
   // ---- fused merge: the last workgroup of a head group combines the splits ----
+  // Every partial of this workgroup was written with an agent-scope atomic
+  // store, which completes at the device-coherent level; waiting for the
+  // stores to complete orders them before this workgroup's arrival on the
+  // counter, so no L2 writeback (the agent-scope release fence) is needed.
+  // The workgroup that arrives last reads every partial of its head group
+  // with agent-scope atomic loads, which are served from that level too.
   if (!final_out && x.counters) {
     __shared__ unsigned s_last;
     unsigned *cnt = x.counters + (long long)b * gridDim.y + hb;
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent"); // this thread's partials
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();
     if (threadIdx.x == 0)
-      s_last = __hip_atomic_fetch_add(cnt, 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT) ==
+      s_last = __hip_atomic_fetch_add(cnt, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
                (unsigned)(a.splits - 1);
     __syncthreads();
     if (s_last) {
-      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent"); // everyone else's partials
-      const int h_first = G > 1 ? hkv * G : hb;
-      for (int hh = 0; hh < G; ++hh)
-        merge_head<D, WPB * 64>(a, x, (long long)b * a.H + h_first + hh, smem);
+      merge_group<D, G, WPB * 64>(a, x, (long long)b * a.H + (G > 1 ? hkv * G : hb), smem);
       if (threadIdx.x == 0)
         __hip_atomic_store(cnt, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+  }
+}
+
+// Fused-step merge of the G heads [head0, head0 + G) by the last workgroup
+// of their head group: the same log-sum-exp recombination as decode_merge,
+// with every partial read through agent-scope atomic loads. Thread t owns
+// output elements t, t + NT, ...; it issues the loads of a chunk of splits
+// for all of them while the split maxima and sums of every head are loaded
+// into LDS, so a chunk costs one memory round trip. `lds` holds 2*G*S + G
+// floats.
+template <int D, int G, int NT>
+__device__ void merge_group(const Args &a, const Ext &x, long long head0, float *lds) {
+  constexpr int EPT = (G * D + NT - 1) / NT;   // output elements per thread
+  constexpr int MC = EPT >= 4 ? 8 : 32 / EPT;  // splits per chunk
+  const int S = a.splits, tid = threadIdx.x;
+  float *sm = lds, *sl = lds + G * S, *sL = lds + 2 * G * S;
+  auto ld = [](const float *p) __attribute__((always_inline)) {
+    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  };
+  for (int i = tid; i < G * S; i += NT) {
+    const float *ml = a.part_ml + ((head0 + i / S) * S + i % S) * 2;
+    sm[i] = ld(ml);
+    sl[i] = ld(ml + 1);
+  }
+  __syncthreads();
+  // per head: max, split weights (in place of the maxima) and the sum
+  for (int h = tid >> 6; h < G; h += NT / 64) {
+    const int lane = tid & 63;
+    float M = -INFINITY;
+    for (int s = lane; s < S; s += 64) M = fmaxf(M, sm[h * S + s]);
+#pragma unroll
+    for (int m = 1; m < 64; m <<= 1) M = fmaxf(M, __shfl_xor(M, m));
+    float L = 0.f;
+    for (int s = lane; s < S; s += 64) {
+      const float ms = sm[h * S + s];
+      const float w = ms == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(ms - M);
+      sm[h * S + s] = w;
+      L = fmaf(sl[h * S + s], w, L);
+    }
+#pragma unroll
+    for (int m = 1; m < 64; m <<= 1) L += __shfl_xor(L, m);
+    if (lane == 0) sL[h] = L;
+  }
+  __syncthreads();
+  float O[EPT];
+#pragma unroll
+  for (int e = 0; e < EPT; ++e) O[e] = 0.f;
+  for (int s0 = 0; s0 < S; s0 += MC) {
+    float o[EPT][MC];
+#pragma unroll
+    for (int e = 0; e < EPT; ++e) {
+      const int el = tid + e * NT;
+#pragma unroll
+      for (int i = 0; i < MC; ++i) {
+        const int s = s0 + i;
+        o[e][i] = (el < G * D && s < S)
+                      ? ld(a.part_o + ((head0 + el / D) * S + s) * D + el % D) : 0.f;
+      }
+    }
+#pragma unroll
+    for (int e = 0; e < EPT; ++e) {
+      const int el = tid + e * NT;
+      const int h = el < G * D ? el / D : 0;
+#pragma unroll
+      for (int i = 0; i < MC; ++i)
+        if (s0 + i < S) O[e] = fmaf(o[e][i], sm[h * S + s0 + i], O[e]);
+    }
+  }
+#pragma unroll
+  for (int e = 0; e < EPT; ++e) {
+    const int el = tid + e * NT;
+    if (el < G * D) {
+      const float L = sL[el / D];
+      const float res = L > 0.f ? O[e] / L : 0.f;
+      const long long head = head0 + el / D;
+      if (x.out16) x.out16[head * D + el % D] = (_Float16)res;
+      else a.out[head * D + el % D] = res;
     }
   }
 }
@@ -890,11 +985,15 @@ hipError_t launch_group(const Args &a, const Ext &x, const Launch &l, hipStream_
   const dim3 grid(a.splits, G > 1 ? a.Hkv : a.H, a.B);
   const dim3 block(a.warps * 64);
   const int final_out = (a.splits == 1 && !l.partial_only) ? 1 : 0;
-  const bool fused = x.counters && !final_out && !l.partial_only;
+  // the fused step keeps every head group's split maxima, sums and weights in
+  // LDS; beyond 64 KiB of them the step runs as two launches (the counters
+  // are then left untouched, at zero)
+  const bool fused = x.counters && !final_out && !l.partial_only &&
+                     (size_t)(2 * G * a.splits + G) * sizeof(float) <= 65536;
   Ext xk = x;
   if (!fused) xk.counters = nullptr;
   size_t lds = combine_lds<FMT, D, GQ, G>(a.warps);
-  if (fused) lds = std::max(lds, (size_t)(a.splits + a.warps * 64) * sizeof(float));
+  if (fused) lds = std::max(lds, (size_t)(2 * G * a.splits + G) * sizeof(float));
   auto kernel = a.warps == 4 ? &decode_partial<FMT, D, GQ, G, U, ORD, PAGED, 4>
                              : &decode_partial<FMT, D, GQ, G, U, ORD, PAGED, 8>;
   if (l.ev_start || l.ev_stop)

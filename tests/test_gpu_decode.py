@@ -238,8 +238,16 @@ def test_fused_merge_matches_two_launch(fmt, group, order, bt, G):
         two = run(b, splits, pack=G > 1, unroll=unroll, warps=warps)
         b.out.fill_(float("nan"))
         a = args(b, splits, warps)
-        for _ in range(2):  # the second call reuses the counters left at zero
-            R.launch_fused(vid(b, G > 1, unroll), a, counters)
+        # the first call runs on another query, so its partials differ from the
+        # second call's: a merge that read a stale partial from the first call
+        # (same buffers, counters left at zero) would not match the two-launch
+        # step
+        q_saved = b.q.clone()
+        b.q.mul_(-0.5)
+        R.launch_fused(vid(b, G > 1, unroll), a, counters)
+        torch.cuda.synchronize()
+        b.q.copy_(q_saved)
+        R.launch_fused(vid(b, G > 1, unroll), a, counters)
         torch.cuda.synchronize()
         fused = b.out.cpu().numpy()
         assert int(counters.abs().sum()) == 0
