@@ -19,8 +19,11 @@ rate, not Python's launch rate. HIP events bracket the K steps and, inside
 each step, the split kernel alone (the roofline's dominant kernel).
 
 The CPU baseline times the oracle's restatement of reference_attention
-(runtime/kvf_host.h:202-234, double precision, one core) on the same
-dequantised cache.
+(runtime/kvf_host.h:202-234, double precision) on the same dequantised cache,
+on every host core this job may use (OMP_NUM_THREADS, else all) and on one
+core. Beside the measurement, config.cost_model gives the kvf planner's
+predicted time for the benchmarked plan and the planner's own top-1 plan
+(machines/mi355x.gpu, kvforge_amd/model/constants_mi355x.cal).
 """
 import argparse
 import ctypes
@@ -271,6 +274,7 @@ def main():
         },
         "cpu_baseline": None,
     }
+    result["config"]["cost_model"] = _cost_model(args, H, Hkv, D, n, group, bt, vid, S)
     if args.cpu_seconds > 0:
         result["cpu_baseline"] = _cpu_baseline(args, K, V, q, fmt, group, D, step_ms, q_)
     print(json.dumps(result), flush=True)
@@ -291,29 +295,83 @@ def _traffic_from_profiles(vid, n):
 
 
 def _cpu_baseline(args, K, V, q, fmt, group, D, step_ms, quiet):
-    """Oracle reference_attention on the dequantised cache, one core."""
+    """Oracle reference_attention (runtime/kvf_host.h:202-234, double precision)
+    on the dequantised cache: one core, then every host core this job may use
+    (the (sequence, head) pairs spread over threads, identical output)."""
     import numpy as np
     sys.path.insert(0, os.path.join(ROOT, "tests"))
     import _oracle as O
     _, kdeq = O.quantize(fmt, group, D, K)[::2]
     _, vdeq = O.quantize(fmt, group, D, V)[::2]
-    times = []
-    t_end = time.perf_counter() + args.cpu_seconds
-    while len(times) < 3 or (time.perf_counter() < t_end and len(times) < 50):
-        t0 = time.perf_counter()
-        O.reference_attention(q, kdeq, vdeq)
-        times.append(time.perf_counter() - t0)
-    med = statistics.median(times)
-    log(f"cpu reference_attention: {med * 1e3:.1f} ms/step over {len(times)} reps", quiet=quiet)
+    threads = int(os.environ.get("OMP_NUM_THREADS") or 0) or (os.cpu_count() or 1)
+    threads = max(1, min(threads, os.cpu_count() or 1))
+
+    def sample(fn, budget):
+        times = []
+        t_end = time.perf_counter() + budget
+        while len(times) < 3 or (time.perf_counter() < t_end and len(times) < 50):
+            t0 = time.perf_counter()
+            fn()
+            times.append(time.perf_counter() - t0)
+        return statistics.median(times), len(times)
+
+    one, n1 = sample(lambda: O.reference_attention(q, kdeq, vdeq), args.cpu_seconds * 0.7)
+    allc, na = sample(lambda: O.reference_attention_mt(q, kdeq, vdeq, threads),
+                      args.cpu_seconds * 0.3)
+    log(f"cpu reference_attention: {one * 1e3:.1f} ms/step on 1 core ({n1} reps), "
+        f"{allc * 1e3:.2f} ms/step on {threads} threads ({na} reps)", quiet=quiet)
     return {
-        "value": round(med * 1e6, 1),
+        "value": round(allc * 1e6, 1),
         "unit": "us/step",
-        "cores": 1,
+        "cores": threads,
         "kind": "port",
         "sample": f"full decode step (double-precision reference_attention over the dequantised "
-                  f"cache), median of {len(times)} reps",
-        "gpu_speedup": round(med * 1e3 / step_ms, 1),
+                  f"cache, every (sequence, head) pair), median of {na} reps on {threads} threads; "
+                  f"1 core: median of {n1} reps",
+        "single_core_us": round(one * 1e6, 1),
+        "gpu_speedup": round(allc * 1e3 / step_ms, 1),
     }
+
+
+def _cost_model(args, H, Hkv, D, n, group, bt, vid, S):
+    """The kvf planner's prediction for the benchmarked plan and its own top-1
+    plan for the same shape (MI355X machine file and fitted constants), or
+    None when the compiler binary is not built."""
+    import csv
+    import subprocess
+    import tempfile
+    kvf = os.path.join(ROOT, "kvforge_amd", "bin", "kvf")
+    if not os.path.exists(kvf):
+        return None
+    spec = (f"decode bench(H: {H}, H_kv: {Hkv}, d: {D}, n: {n}) {{\n"
+            f"  Q: query<H, d, f32>\n  K: kvcache<n, d, ?, ?, ?>\n  V: kvcache<n, d, ?, ?, ?>\n"
+            f"  O = decode_attn(Q, K, V, scale = auto, splits = ?, gqa_pack = ?)\n}}\n")
+    with tempfile.TemporaryDirectory() as tmp:
+        path = os.path.join(tmp, "bench.kv")
+        with open(path, "w") as f:
+            f.write(spec)
+        r = subprocess.run([kvf, "plan", path, "--quant", "--all", "--out", tmp,
+                            "--machine", os.path.join(ROOT, "machines", "mi355x.gpu"),
+                            "--calib", os.path.join(ROOT, "kvforge_amd", "model", "constants_mi355x.cal")],
+                           capture_output=True, text=True)
+        if r.returncode != 0:
+            return None
+        with open(os.path.join(tmp, "plans.csv")) as f:
+            rows = list(csv.DictReader(f))
+    fmt_name = vid.split("_")[0]
+    want = {"fmt": fmt_name, "group": str(group), "order": "head_major" if args.order == "hm" else "token_major",
+            "residency": "paged" if bt else "contiguous", "block_tokens": str(bt), "splits": str(S),
+            "gqa_pack": str(args.pack), "warps": str(args.warps), "unroll": str(args.unroll)}
+    mine = next((r for r in rows if all(r[k] == v for k, v in want.items())), None)
+    live = [r for r in rows if r["rejected"] == "0"]
+    best = min(live, key=lambda r: float(r["pred_us"])) if live else None
+    out = {"predicted_us_per_step": round(float(mine["pred_us"]), 3) if mine else None}
+    if best:
+        out["model_top1"] = (f"{best['fmt']}:{best['group']} {best['order']}/{best['residency']} "
+                             f"splits={best['splits']} pack={best['gqa_pack']} w{best['warps']} "
+                             f"u{best['unroll']}")
+        out["model_top1_predicted_us"] = round(float(best["pred_us"]), 3)
+    return out
 
 
 if __name__ == "__main__":

@@ -11,6 +11,7 @@
 #include <limits>
 #include <numeric>
 #include <random>
+#include <thread>
 #include <vector>
 
 namespace {
@@ -239,6 +240,32 @@ void kvfo_reference_attention(int B, int H, int Hkv, int D, int n,
       attend_one(D, n, q + ((long long)b * H + h) * D, K + base, V + base, scale,
                  out + ((long long)b * H + h) * D, sc, acc);
     }
+}
+
+// The same computation with the (sequence, head) pairs dealt round-robin to
+// `threads` host threads; each pair's arithmetic is unchanged, so the output
+// is identical to kvfo_reference_attention. Used for the all-cores CPU
+// baseline.
+void kvfo_reference_attention_mt(int B, int H, int Hkv, int D, int n,
+                                 const float *q, const float *K, const float *V,
+                                 float scale, float *out, int threads) {
+  const int gq = H / Hkv;
+  const int pairs = B * H;
+  if (threads < 1) threads = 1;
+  if (threads > pairs) threads = pairs;
+  auto work = [&](int w) {
+    std::vector<double> sc(n), acc(D);
+    for (int i = w; i < pairs; i += threads) {
+      const int b = i / H, h = i % H, hk = h / gq;
+      const long long base = ((long long)b * Hkv + hk) * n * D;
+      attend_one(D, n, q + (long long)i * D, K + base, V + base, scale, out + (long long)i * D,
+                 sc, acc);
+    }
+  };
+  std::vector<std::thread> pool;
+  for (int w = 1; w < threads; ++w) pool.emplace_back(work, w);
+  work(0);
+  for (auto &t : pool) t.join();
 }
 
 void kvfo_reference_attention_varlen(int B, int H, int Hkv, int D, int n_max,

@@ -11,7 +11,8 @@
  *   kvfo_page_table             runtime/kvf_host.h:156-165 (std::shuffle of iota)
  *   kvfo_row_of                 runtime/kvf_host.h:124-135
  *   kvfo_place                  runtime/kvf_host.h:149-197 (host scatter part)
- *   kvfo_reference_attention    runtime/kvf_host.h:202-234
+ *   kvfo_reference_attention    runtime/kvf_host.h:202-234 (and _mt: the
+ *                               same per-head arithmetic over host threads)
  *   kvfo_rel_l2                 runtime/kvf_host.h:236-244
  *   kvfo_reference_partials     runtime/kvf_kernels.cuh:147-153,276-281 (split
  *                               chunking, per-split max/sum in the log2 domain)
@@ -84,6 +85,10 @@ void kvfo_reference_attention(int B, int H, int Hkv, int D, int n,
 
 /* Variable-length extension (this build's definition): sequence b uses the
  * first lens[b] tokens of its rows; K/V are [B][Hkv][n_max][D]. */
+/* As kvfo_reference_attention, over `threads` host threads (same output). */
+void kvfo_reference_attention_mt(int B, int H, int Hkv, int D, int n,
+                                 const float *q, const float *K, const float *V,
+                                 float scale, float *out, int threads);
 void kvfo_reference_attention_varlen(int B, int H, int Hkv, int D, int n_max,
                                      const int32_t *lens, const float *q,
                                      const float *K, const float *V,

@@ -56,6 +56,7 @@ def lib():
         "kvfo_place": (None, [_i, _i, _i, _i, _i, _i, _i, _p, _i, _p, _p, _p, _p]),
         "kvfo_reference_attention": (None, [_i, _i, _i, _i, _i, _p, _p, _p, _f, _p]),
         "kvfo_reference_attention_varlen": (None, [_i, _i, _i, _i, _i, _p, _p, _p, _p, _f, _p]),
+        "kvfo_reference_attention_mt": (None, [_i, _i, _i, _i, _i, _p, _p, _p, _f, _p, _i]),
         "kvfo_rel_l2": (_d, [_p, _p, _ll]),
         "kvfo_scale_log2": (_f, [_i]),
         "kvfo_reference_partials": (None, [_i, _i, _i, _i, _i, _i, _p, _p, _p, _f, _p, _p, _p]),
@@ -170,6 +171,20 @@ def reference_attention(q, K, V, scale=None):
     lib().kvfo_reference_attention(B, H, Hkv, D, n, _ptr(np.ascontiguousarray(q)),
                                    _ptr(np.ascontiguousarray(K)),
                                    _ptr(np.ascontiguousarray(V)), scale, _ptr(out))
+    return out
+
+
+def reference_attention_mt(q, K, V, threads, scale=None):
+    """reference_attention with the (sequence, head) pairs spread over host
+    threads; the output is identical."""
+    B, H, D = q.shape
+    _, Hkv, n, _ = K.shape
+    if scale is None:
+        scale = float(np.float32(1.0) / np.sqrt(np.float32(D)))
+    out = np.empty((B, H, D), dtype=np.float32)
+    lib().kvfo_reference_attention_mt(B, H, Hkv, D, n, _ptr(np.ascontiguousarray(q)),
+                                      _ptr(np.ascontiguousarray(K)),
+                                      _ptr(np.ascontiguousarray(V)), scale, _ptr(out), threads)
     return out
 
 

@@ -236,6 +236,14 @@ def test_attention_matches_scipy_softmax():
     assert np.max(np.abs(got - ref)) < 1e-6
 
 
+def test_attention_threaded_is_identical():
+    # the all-cores CPU baseline: same per-head arithmetic, any thread count
+    q, K, V = O.make_data(2, 12, 3, 128, 257, seed=6)
+    one = O.reference_attention(q, K, V)
+    for threads in (1, 3, 8, 64):
+        assert np.array_equal(O.reference_attention_mt(q, K, V, threads), one)
+
+
 def test_attention_closed_forms():
     rng = np.random.default_rng(9)
     D = 128
