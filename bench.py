@@ -1,22 +1,33 @@
 #!/usr/bin/env python3
 """Decode-step benchmark of the MI355X split-KV decode-attention path.
 
-Workload (the north-star shape): Llama-3-8B-shaped
-GQA decode, 32 query heads over 8 KV heads, head dimension 128, batch 1,
-32768 cached tokens, K/V ~ N(0,1) from the reference generator
-(runtime/kvf_host.h:51-61, seed 1) with 1% outlier channels x8, quantized
-int8:G=64 on the GPU by the product's quantize/place kernel, head-major
-contiguous. One step = one decode-attention call of the plan (the split
-kernel plus the log-sum-exp merge), exactly what the reference's generated
-kvf_launch_<name> enqueues (runtime/kvf_kernels.cuh:309-320).
+Workloads (--config selects, 2 is the default and the
+one the headline metric is quoted on):
+
+  2  Llama-3-8B-shaped GQA decode: 32 query heads over 8 KV heads, head dim
+     128, batch 1, 32768 cached tokens, K/V ~ N(0,1) from the reference
+     generator (runtime/kvf_host.h:51-61, seed 1) with 1% outlier channels x8,
+     quantized int8:G=64 on the GPU by the product's quantize/place kernel,
+     head-major contiguous; plan int8_hm_c_g4_u2_d128, 32 splits.
+  3  Paged batched GQA decode: batch 8, lengths uniform in [2048, 8192] (seed
+     2), one shared pool of 4096 pages of 16 tokens shuffled with seed 18 and
+     handed out in order, token-major int8:64, binary16 query and output,
+     through the variable-length extension.
+  4  Long-context GQA decode: batch 1, 65536 tokens, int4:G=32 head-major
+     contiguous.
+
+One step = one decode-attention call of the plan (the split kernel plus the
+log-sum-exp merge), exactly what the reference's generated kvf_launch_<name>
+enqueues (runtime/kvf_kernels.cuh:309-320).
 
 Timing. The cache is replicated into enough copies that consecutive steps
 never find their bytes in the 256 MiB Infinity Cache (the reference flushes
 with a memset instead, runtime/kvf_host.h:302-331; a rotation keeps the flush
 out of the timed region). The GPU is held behind a spin kernel while the
 host enqueues all K steps, so the timed region is the GPU's own back-to-back
-rate, not Python's launch rate. HIP events bracket the K steps and, inside
-each step, the split kernel alone (the roofline's dominant kernel).
+rate, not Python's launch rate. HIP events bracket the K steps and, in a
+second pass, the split kernel alone (the roofline's dominant kernel), bound to
+its own dispatch.
 
 The CPU baseline times the oracle's restatement of reference_attention
 (runtime/kvf_host.h:202-234, double precision) on the same dequantised cache,
@@ -33,6 +44,7 @@ import os
 import statistics
 import sys
 import time
+import types
 
 ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
@@ -40,6 +52,11 @@ sys.path.insert(0, ROOT)
 HBM_PEAK_GBS = 8000.0
 METRIC = ("\u00b5s/decode step + achieved HBM GB/s (% of peak), "
           "GQA32/8 d128 32k int8:64")
+CONFIG_DEFAULTS = {  # config -> (fmt, group, n, order, block tokens, splits)
+    2: ("int8", 64, 32768, "hm", 0, 32),
+    3: ("int8", 64, 8192, "tm", 16, 4),
+    4: ("int4", 32, 65536, "hm", 0, 32),
+}
 
 
 def parse():
@@ -47,12 +64,14 @@ def parse():
     p.add_argument("--gpus", type=int, default=1)
     p.add_argument("--steps", type=int, default=400)
     p.add_argument("--warmup", type=int, default=50)
-    p.add_argument("--fmt", default="int8", choices=["f16", "int8", "int4"])
-    p.add_argument("--group", type=int, default=64)
-    p.add_argument("--n", type=int, default=32768)
-    p.add_argument("--order", default="hm", choices=["hm", "tm"])
-    p.add_argument("--block-tokens", type=int, default=0)
-    p.add_argument("--splits", type=int, default=32)
+    p.add_argument("--config", type=int, default=2, choices=sorted(CONFIG_DEFAULTS))
+    p.add_argument("--fmt", default=None, choices=["f16", "int8", "int4"])
+    p.add_argument("--group", type=int, default=None)
+    p.add_argument("--n", type=int, default=None,
+                   help="tokens (configs 2 and 4; config 3 draws its lengths)")
+    p.add_argument("--order", default=None, choices=["hm", "tm"])
+    p.add_argument("--block-tokens", type=int, default=None)
+    p.add_argument("--splits", type=int, default=None)
     p.add_argument("--warps", type=int, default=4)
     p.add_argument("--unroll", type=int, default=2)
     p.add_argument("--pack", type=int, default=1)
@@ -64,12 +83,126 @@ def parse():
                    help="time the one-launch fused-merge entry point instead of the drop-in "
                         "two-launch kvf_launch_variant")
     p.add_argument("--json-only", action="store_true")
-    return p.parse_args()
+    a = p.parse_args()
+    fmt, group, n, order, bt, splits = CONFIG_DEFAULTS[a.config]
+    a.fmt = a.fmt or fmt
+    a.group = a.group if a.group is not None else group
+    a.n = a.n or n
+    a.order = a.order or order
+    a.block_tokens = a.block_tokens if a.block_tokens is not None else bt
+    a.splits = a.splits or splits
+    return a
 
 
 def log(*a, quiet=False):
     if not quiet:
         print(*a, file=sys.stderr, flush=True)
+
+
+def build_workload(args, R, torch, np):
+    """Inputs of the selected config, quantized and placed on the GPU by the
+    product's own append kernel, replicated for the cache rotation."""
+    host = R.host_lib()
+    P = ctypes.c_void_p
+    dev = torch.device("cuda:0")
+    W = types.SimpleNamespace()
+    W.B = 8 if args.config == 3 else 1
+    W.H, W.Hkv, W.D = 32, 8, 128
+    W.fmt = R.FMT_BY_NAME[args.fmt]
+    W.group = args.group if W.fmt != R.FMT_F16 else 0
+    W.order = R.ORD_HEAD if args.order == "hm" else R.ORD_TOKEN
+    W.bt = args.block_tokens
+    B, H, Hkv, D = W.B, W.H, W.Hkv, W.D
+    if args.config == 3:
+        lens = np.empty(B, np.int32)
+        host.kvfh_varlen_lengths(B, 2048, 8192, 2, P(lens.ctypes.data))
+        W.lens = lens
+        W.n = int(lens.max())
+    else:
+        W.lens = None
+        W.n = args.n
+    n = W.n
+    q = np.empty((B, H, D), np.float32)
+    K = np.empty((B, Hkv, n, D), np.float32)
+    V = np.empty((B, Hkv, n, D), np.float32)
+    host.kvfh_make_data(B, H, Hkv, D, n, 1, P(q.ctypes.data), P(K.ctypes.data), P(V.ctypes.data))
+    if args.config == 2:
+        host.kvfh_inject_outliers(B, Hkv, D, n, 1001, 0.01, 8.0, P(K.ctypes.data), P(V.ctypes.data))
+    W.q, W.K, W.V = q, K, V
+    rb = R.row_bytes(W.fmt, D)
+    mw = D // W.group if W.group else 0
+    W.rb, W.mw = rb, mw
+    if args.config == 3:
+        pool = 4096
+        mb = (W.n + W.bt - 1) // W.bt
+        tbl = np.empty(B * mb, np.int32)
+        used = host.kvfh_pool_table(B, P(lens.ctypes.data), W.bt, pool, 18, mb, P(tbl.ctypes.data))
+        if used < 0:
+            raise SystemExit("block pool too small")
+        rows = pool * Hkv * W.bt
+        W.table = torch.from_numpy(np.where(tbl < 0, 0, tbl).astype(np.int32)).to(dev)
+        W.max_blocks = mb
+    else:
+        rows, W.max_blocks = R.rows_alloc(B, Hkv, n, W.bt)
+        W.table = None
+        if W.bt:
+            tbl = np.empty(B * W.max_blocks, np.int32)
+            host.kvfh_page_table(B * W.max_blocks, 18, P(tbl.ctypes.data))
+            W.table = torch.from_numpy(tbl).to(dev)
+    k0 = torch.zeros(rows * rb, dtype=torch.uint8, device=dev)
+    v0 = torch.zeros(rows * rb, dtype=torch.uint8, device=dev)
+    km0 = torch.zeros(rows * mw, dtype=torch.int32, device=dev) if mw else None
+    vm0 = torch.zeros(rows * mw, dtype=torch.int32, device=dev) if mw else None
+    for src, dst, dm in ((K, k0, km0), (V, v0, vm0)):
+        if args.config == 3:  # each sequence appends only its own tokens into its own pages
+            for b in range(B):
+                L = int(lens[b])
+                x = torch.from_numpy(np.ascontiguousarray(src[b, :, :L])).to(dev)
+                R.quantize_place(W.fmt, W.group, D, x, 1, Hkv, L, W.order, W.bt, W.table[b],
+                                 W.max_blocks, dst, dm)
+        else:
+            x = torch.from_numpy(src).to(dev)
+            R.quantize_place(W.fmt, W.group, D, x, B, Hkv, n, W.order, W.bt, W.table,
+                             W.max_blocks, dst, dm)
+        del x
+    torch.cuda.synchronize()
+    # algorithmic bytes per step (runtime/kvf_driver.cu:51: KV payload + group meta)
+    tokens = int(lens.sum()) if args.config == 3 else B * n
+    W.alg_bytes = 2 * tokens * Hkv * (rb + mw * 4)
+    cache_bytes = 2 * rows * (rb + mw * 4)
+    W.copies = args.copies or max(4, math.ceil((1 << 30) / cache_bytes))
+    W.caches = [(k0, v0, km0, vm0)]
+    for _ in range(W.copies - 1):
+        W.caches.append(tuple(t.clone() if t is not None else None for t in (k0, v0, km0, vm0)))
+    W.G = H // Hkv if args.pack else 1
+    W.vid = R.variant_id(W.fmt, W.order, W.bt > 0, W.G, args.unroll, D)
+    W.qd = torch.from_numpy(q).to(dev)
+    W.out = torch.zeros((B, H, D), dtype=torch.float32, device=dev)
+    if args.config == 3:
+        W.q16 = torch.from_numpy(q.astype(np.float16)).to(dev)
+        W.out16 = torch.zeros((B, H, D), dtype=torch.float16, device=dev)
+        W.lens_d = torch.from_numpy(lens).to(dev)
+        W.va = R.VarlenArgs()
+        W.va.seq_lens = W.lens_d.data_ptr()
+        W.va.q16 = W.q16.data_ptr()
+        W.va.out16 = W.out16.data_ptr()
+    else:
+        W.va = None
+    if args.config == 2:
+        W.data = "synthetic: reference generator seed 1 + 1% outlier channels x8"
+        W.workload = (f"GQA{H}/{Hkv} d{D} n{n} B{B} {args.fmt}{':' + str(W.group) if W.group else ''} "
+                      f"{args.order}/{'paged:%d' % W.bt if W.bt else 'contiguous'}")
+    elif args.config == 3:
+        W.data = ("synthetic: reference generator seed 1, lengths U[2048, 8192] seed 2, "
+                  "4096-page pool shuffled with seed 18")
+        W.workload = (f"GQA{H}/{Hkv} d{D} B{B} lengths {int(lens.min())}..{int(lens.max())} "
+                      f"(sum {int(lens.sum())}) {args.fmt}:{W.group} {args.order}/paged:{W.bt} "
+                      f"pool 4096, f16 q/out")
+    else:
+        W.data = "synthetic: reference generator seed 1"
+        W.workload = (f"GQA{H}/{Hkv} d{D} n{n} B{B} {args.fmt}:{W.group} "
+                      f"{args.order}/{'paged:%d' % W.bt if W.bt else 'contiguous'}")
+    return W
 
 
 def main():
@@ -83,81 +216,60 @@ def main():
     from kvforge_amd import runtime as R
 
     q_ = args.json_only
-    B, H, Hkv, D, n = 1, 32, 8, 128, args.n
-    fmt = R.FMT_BY_NAME[args.fmt]
-    group = args.group if fmt != R.FMT_F16 else 0
-    order = R.ORD_HEAD if args.order == "hm" else R.ORD_TOKEN
-    bt = args.block_tokens
-    G = H // Hkv if args.pack else 1
-    vid = R.variant_id(fmt, order, bt > 0, G, args.unroll, D)
-    dev = torch.device("cuda:0")
     R.hip_lib()
-    host = R.host_lib()
-
-    # ---- inputs: reference generator + outlier channels, quantized on GPU ----
     t_prep = time.perf_counter()
-    q = np.empty((B, H, D), np.float32)
-    K = np.empty((B, Hkv, n, D), np.float32)
-    V = np.empty((B, Hkv, n, D), np.float32)
-    P = ctypes.c_void_p
-    host.kvfh_make_data(B, H, Hkv, D, n, 1, P(q.ctypes.data), P(K.ctypes.data), P(V.ctypes.data))
-    host.kvfh_inject_outliers(B, Hkv, D, n, 1001, 0.01, 8.0, P(K.ctypes.data), P(V.ctypes.data))
-    rows, mb = R.rows_alloc(B, Hkv, n, bt)
-    table = None
-    if bt:
-        tbl = np.empty(B * mb, np.int32)
-        host.kvfh_page_table(B * mb, 18, P(tbl.ctypes.data))
-        table = torch.from_numpy(tbl).to(dev)
-    rb = R.row_bytes(fmt, D)
-    mw = D // group if group else 0
-    k0 = torch.zeros(rows * rb, dtype=torch.uint8, device=dev)
-    v0 = torch.zeros(rows * rb, dtype=torch.uint8, device=dev)
-    km0 = torch.zeros(rows * mw, dtype=torch.int32, device=dev) if mw else None
-    vm0 = torch.zeros(rows * mw, dtype=torch.int32, device=dev) if mw else None
-    for src, dst, dm in ((K, k0, km0), (V, v0, vm0)):
-        x = torch.from_numpy(src).to(dev)
-        R.quantize_place(fmt, group, D, x, B, Hkv, n, order, bt, table, mb, dst, dm)
-        del x
-    torch.cuda.synchronize()
-    qd = torch.from_numpy(q).to(dev)
+    W = build_workload(args, R, torch, np)
     log(f"inputs ready in {time.perf_counter() - t_prep:.1f} s", quiet=q_)
-
-    # algorithmic bytes per step (runtime/kvf_driver.cu:51: KV payload + group meta)
-    alg_bytes = 2 * B * n * Hkv * (rb + mw * 4)
-    cache_bytes = alg_bytes if not bt else 2 * rows * (rb + mw * 4)
-    copies = args.copies or max(4, math.ceil((1 << 30) / cache_bytes))
-    caches = [(k0, v0, km0, vm0)]
-    for _ in range(copies - 1):
-        caches.append(tuple(t.clone() if t is not None else None for t in (k0, v0, km0, vm0)))
-    S = args.splits
-    out = torch.zeros((B, H, D), dtype=torch.float32, device=dev)
+    B, H, Hkv, D, n, S = W.B, W.H, W.Hkv, W.D, W.n, args.splits
+    dev = W.out.device
+    copies = W.copies
     part_o = torch.zeros((B, H, S, D), dtype=torch.float32, device=dev)
     part_ml = torch.zeros((B, H, S, 2), dtype=torch.float32, device=dev)
-    arg_list = [R.make_args(qd, k, v, km, vm, table, out, part_o, part_ml, B, H, Hkv, n, S,
-                            args.warps, group=group, block_tokens=bt, max_blocks=mb, D=D)
-                for (k, v, km, vm) in caches]
+    arg_list = [R.make_args(W.qd, k, v, km, vm, W.table, W.out, part_o, part_ml, B, H, Hkv, n, S,
+                            args.warps, group=W.group, block_tokens=W.bt, max_blocks=W.max_blocks,
+                            D=D)
+                for (k, v, km, vm) in W.caches]
     L = R.hip_lib()
-    vb = vid.encode()
+    vb = W.vid.encode()
+    vid = W.vid
     st = torch.cuda.current_stream()
     sh = ctypes.c_void_p(st.cuda_stream)
-    launch_step = L.kvf_launch_variant
-    launch_timed = L.kvf_launch_partial_variant_timed
     refs = [ctypes.byref(a) for a in arg_list]
+    va = ctypes.byref(W.va) if W.va is not None else None
+    out_t = W.out16 if W.va is not None else W.out
+
+    if W.va is not None:
+        def launch_step(i):
+            return L.kvf_launch_varlen_variant(vb, refs[i % copies], va, sh)
+
+        def launch_timed(i, e0, e1):
+            return L.kvf_launch_partial_varlen_variant_timed(vb, refs[i % copies], va, sh, e0, e1)
+    else:
+        def launch_step(i):
+            return L.kvf_launch_variant(vb, refs[i % copies], sh)
+
+        def launch_timed(i, e0, e1):
+            return L.kvf_launch_partial_variant_timed(vb, refs[i % copies], sh, e0, e1)
 
     def step(i):
-        e = launch_step(vb, refs[i % copies], sh)
+        e = launch_step(i)
         if e:
-            raise R.KvfError(f"kvf_launch_variant({vid}) failed: {e}")
+            raise R.KvfError(f"decode step of {vid} failed: {e}")
 
     # correctness guard: the plan's output must match a single-split run
     step(0)
     torch.cuda.synchronize()
-    got = out.clone()
-    a1 = R.make_args(qd, k0, v0, km0, vm0, table, out, None, None, B, H, Hkv, n, 1, 4,
-                     group=group, block_tokens=bt, max_blocks=mb, D=D)
-    R.launch(R.variant_id(fmt, order, bt > 0, G, 2, D), a1)
+    got = out_t.float().clone()
+    a1 = R.make_args(W.qd, *W.caches[0], W.table, W.out, None, None, B, H, Hkv, n, 1, 4,
+                     group=W.group, block_tokens=W.bt, max_blocks=W.max_blocks, D=D)
+    v1 = R.variant_id(W.fmt, W.order, W.bt > 0, W.G, 2, D)
+    if W.va is not None:
+        R.check(L.kvf_launch_varlen_variant(v1.encode(), ctypes.byref(a1), va, sh), "S=1 step")
+    else:
+        R.launch(v1, a1)
     torch.cuda.synchronize()
-    rel = float(torch.linalg.vector_norm(got - out) / torch.linalg.vector_norm(out))
+    ref1 = out_t.float()
+    rel = float(torch.linalg.vector_norm(got - ref1) / torch.linalg.vector_norm(ref1))
     if not (rel < 2e-3 and bool(torch.isfinite(got).all())):
         raise SystemExit(f"plan {vid} S={S} disagrees with S=1: rel_l2 {rel}")
 
@@ -167,20 +279,20 @@ def main():
     K_ = args.steps
 
     # fused path: one launch per step, split merge inside the kernel
+    G = W.G
     counters = torch.zeros(B * (Hkv if G > 1 else H), dtype=torch.int32, device=dev)
-    launch_fused = L.kvf_launch_fused_variant
     cptr = ctypes.c_void_p(counters.data_ptr())
 
     def step_fused(i):
-        e = launch_fused(vb, refs[i % copies], None, cptr, sh)
+        e = L.kvf_launch_fused_variant(vb, refs[i % copies], va, cptr, sh)
         if e:
             raise R.KvfError(f"kvf_launch_fused_variant({vid}) failed: {e}")
 
     if S > 1 and args.fused:
-        out.zero_()
+        out_t.zero_()
         step_fused(0)
         torch.cuda.synchronize()
-        relf = float(torch.linalg.vector_norm(got - out) / torch.linalg.vector_norm(got))
+        relf = float(torch.linalg.vector_norm(got - out_t.float()) / torch.linalg.vector_norm(got))
         if not (relf < 1e-5 and int(counters.abs().sum()) == 0):
             raise SystemExit(f"fused step disagrees with the two-launch step: {relf}")
         for i in range(args.warmup):
@@ -213,8 +325,8 @@ def main():
         path = "kvf_launch_fused_variant (one launch, in-kernel split merge)"
     else:
         step_ms, wall_t = step2_ms, wall_2
-        path = "kvf_launch_variant (split kernel + merge kernel)"
-    wall0, wall1 = 0.0, wall_t
+        path = ("kvf_launch_varlen_variant" if W.va is not None else "kvf_launch_variant") + \
+            " (split kernel + merge kernel)"
 
     # ---- the split kernel alone, K launches, each timed by events bound to
     # its own dispatch (the duration a kernel trace reports) ------------------
@@ -226,16 +338,17 @@ def main():
     torch.cuda.synchronize()
     torch.cuda._sleep(int(5e7))
     for i in range(K_):
-        e = launch_timed(vb, refs[i % copies], sh, kev[i][0], kev[i][1])
+        e = launch_timed(i, kev[i][0], kev[i][1])
         if e:
-            raise R.KvfError(f"kvf_launch_partial_variant_timed failed: {e}")
+            raise R.KvfError(f"timed split-kernel launch failed: {e}")
     torch.cuda.synchronize()
     part_ms = [e0.elapsed_time(e1) for e0, e1 in kev]
     part_avg_us = 1e3 * sum(part_ms) / K_
     part_med_us = 1e3 * statistics.median(part_ms)
 
+    alg_bytes = W.alg_bytes
     achieved = alg_bytes / (part_avg_us * 1e-6) / 1e9
-    traffic = _traffic_from_profiles(vid, n)
+    traffic = _traffic_from_profiles(vid, n) if args.config == 2 else None
     result = {
         "metric": METRIC,
         "value": round(step_ms * 1e3, 3),
@@ -247,11 +360,11 @@ def main():
         "higher_is_better": False,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "u8" if fmt == R.FMT_INT8 else ("u4" if fmt == R.FMT_INT4 else "f16"),
-        "data": "synthetic: reference generator seed 1 + 1% outlier channels x8",
+        "dtype": "u8" if W.fmt == R.FMT_INT8 else ("u4" if W.fmt == R.FMT_INT4 else "f16"),
+        "data": W.data,
         "config": {
-            "workload": f"GQA{H}/{Hkv} d{D} n{n} B{B} {args.fmt}{':' + str(group) if group else ''} "
-                        f"{args.order}/{'paged:%d' % bt if bt else 'contiguous'}",
+            "workload": W.workload,
+            "baseline_config": args.config,
             "plan": f"{vid} splits={S} waves={args.warps}",
             "entry_point": path,
             "two_launch_us_per_step": round(step2_ms * 1e3, 3),
@@ -261,7 +374,7 @@ def main():
             "partial_kernel_us_avg": round(part_avg_us, 3),
             "partial_kernel_us_median": round(part_med_us, 3),
             "cache_copies_rotated": copies,
-            "wall_s_timed_region": round(wall1 - wall0, 4),
+            "wall_s_timed_region": round(wall_t, 4),
         },
         "roofline": {
             "bound": "hbm",
@@ -274,9 +387,10 @@ def main():
         },
         "cpu_baseline": None,
     }
-    result["config"]["cost_model"] = _cost_model(args, H, Hkv, D, n, group, bt, vid, S)
+    n_model = int(round(float(W.lens.mean()))) if W.lens is not None else n
+    result["config"]["cost_model"] = _cost_model(args, W, n_model, S)
     if args.cpu_seconds > 0:
-        result["cpu_baseline"] = _cpu_baseline(args, K, V, q, fmt, group, D, step_ms, q_)
+        result["cpu_baseline"] = _cpu_baseline(args, W, step_ms, q_)
     print(json.dumps(result), flush=True)
 
 
@@ -294,17 +408,25 @@ def _traffic_from_profiles(vid, n):
     return ent.get("hbm_bytes_per_launch") if ent else None
 
 
-def _cpu_baseline(args, K, V, q, fmt, group, D, step_ms, quiet):
+def _cpu_baseline(args, W, step_ms, quiet):
     """Oracle reference_attention (runtime/kvf_host.h:202-234, double precision)
     on the dequantised cache: one core, then every host core this job may use
     (the (sequence, head) pairs spread over threads, identical output)."""
     import numpy as np
     sys.path.insert(0, os.path.join(ROOT, "tests"))
     import _oracle as O
-    _, kdeq = O.quantize(fmt, group, D, K)[::2]
-    _, vdeq = O.quantize(fmt, group, D, V)[::2]
+    _, kdeq = O.quantize(W.fmt, W.group, W.D, W.K)[::2]
+    _, vdeq = O.quantize(W.fmt, W.group, W.D, W.V)[::2]
     threads = int(os.environ.get("OMP_NUM_THREADS") or 0) or (os.cpu_count() or 1)
     threads = max(1, min(threads, os.cpu_count() or 1))
+    q = W.q
+    if W.lens is not None:  # binary16 query, as the GPU consumes it
+        q = q.astype(np.float16).astype(np.float32)
+        one_fn = lambda: O.reference_attention_varlen(q, kdeq, vdeq, W.lens)  # noqa: E731
+        all_fn = lambda: O.reference_attention_varlen_mt(q, kdeq, vdeq, W.lens, threads)  # noqa: E731
+    else:
+        one_fn = lambda: O.reference_attention(q, kdeq, vdeq)  # noqa: E731
+        all_fn = lambda: O.reference_attention_mt(q, kdeq, vdeq, threads)  # noqa: E731
 
     def sample(fn, budget):
         times = []
@@ -315,9 +437,8 @@ def _cpu_baseline(args, K, V, q, fmt, group, D, step_ms, quiet):
             times.append(time.perf_counter() - t0)
         return statistics.median(times), len(times)
 
-    one, n1 = sample(lambda: O.reference_attention(q, kdeq, vdeq), args.cpu_seconds * 0.7)
-    allc, na = sample(lambda: O.reference_attention_mt(q, kdeq, vdeq, threads),
-                      args.cpu_seconds * 0.3)
+    one, n1 = sample(one_fn, args.cpu_seconds * 0.7)
+    allc, na = sample(all_fn, args.cpu_seconds * 0.3)
     log(f"cpu reference_attention: {one * 1e3:.1f} ms/step on 1 core ({n1} reps), "
         f"{allc * 1e3:.2f} ms/step on {threads} threads ({na} reps)", quiet=quiet)
     return {
@@ -333,17 +454,18 @@ def _cpu_baseline(args, K, V, q, fmt, group, D, step_ms, quiet):
     }
 
 
-def _cost_model(args, H, Hkv, D, n, group, bt, vid, S):
+def _cost_model(args, W, n, S):
     """The kvf planner's prediction for the benchmarked plan and its own top-1
     plan for the same shape (MI355X machine file and fitted constants), or
-    None when the compiler binary is not built."""
+    None when the compiler binary is not built. A variable-length batch is
+    planned at its mean length (the planner models one length per batch)."""
     import csv
     import subprocess
     import tempfile
     kvf = os.path.join(ROOT, "kvforge_amd", "bin", "kvf")
     if not os.path.exists(kvf):
         return None
-    spec = (f"decode bench(H: {H}, H_kv: {Hkv}, d: {D}, n: {n}) {{\n"
+    spec = (f"decode bench(H: {W.H}, H_kv: {W.Hkv}, d: {W.D}, n: {n}, batch: {W.B}) {{\n"
             f"  Q: query<H, d, f32>\n  K: kvcache<n, d, ?, ?, ?>\n  V: kvcache<n, d, ?, ?, ?>\n"
             f"  O = decode_attn(Q, K, V, scale = auto, splits = ?, gqa_pack = ?)\n}}\n")
     with tempfile.TemporaryDirectory() as tmp:
@@ -358,14 +480,16 @@ def _cost_model(args, H, Hkv, D, n, group, bt, vid, S):
             return None
         with open(os.path.join(tmp, "plans.csv")) as f:
             rows = list(csv.DictReader(f))
-    fmt_name = vid.split("_")[0]
-    want = {"fmt": fmt_name, "group": str(group), "order": "head_major" if args.order == "hm" else "token_major",
-            "residency": "paged" if bt else "contiguous", "block_tokens": str(bt), "splits": str(S),
-            "gqa_pack": str(args.pack), "warps": str(args.warps), "unroll": str(args.unroll)}
+    want = {"fmt": W.vid.split("_")[0], "group": str(W.group),
+            "order": "head_major" if args.order == "hm" else "token_major",
+            "residency": "paged" if W.bt else "contiguous", "block_tokens": str(W.bt),
+            "splits": str(S), "gqa_pack": str(args.pack), "warps": str(args.warps),
+            "unroll": str(args.unroll)}
     mine = next((r for r in rows if all(r[k] == v for k, v in want.items())), None)
     live = [r for r in rows if r["rejected"] == "0"]
     best = min(live, key=lambda r: float(r["pred_us"])) if live else None
-    out = {"predicted_us_per_step": round(float(mine["pred_us"]), 3) if mine else None}
+    out = {"predicted_us_per_step": round(float(mine["pred_us"]), 3) if mine else None,
+           "planned_length": n}
     if best:
         out["model_top1"] = (f"{best['fmt']}:{best['group']} {best['order']}/{best['residency']} "
                              f"splits={best['splits']} pack={best['gqa_pack']} w{best['warps']} "

@@ -129,6 +129,14 @@ hipError_t kvf_launch_partial_variant_timed(const char *variant_id, const kvf_ar
                                             hipStream_t stream, hipEvent_t start,
                                             hipEvent_t stop);
 
+/* As kvf_launch_partial_variant_timed, for the variable-length / block-pool
+ * extension (`va` as in kvf_launch_varlen_variant; may be NULL). Harness use,
+ * no counterpart in the reference. */
+hipError_t kvf_launch_partial_varlen_variant_timed(const char *variant_id, const kvf_args_t *a,
+                                                   const kvf_varlen_args_t *va,
+                                                   hipStream_t stream, hipEvent_t start,
+                                                   hipEvent_t stop);
+
 /* Only the log-sum-exp merge (runtime/kvf_kernels.cuh:288-306) of the
  * partials named by `a` (B, H, splits, part_o, part_ml, out) for head
  * dimension d. */

@@ -189,6 +189,21 @@ extern "C" hipError_t kvf_launch_partial_variant_timed(const char *id, const kvf
   return fx(*a, Ext{}, l, st);
 }
 
+extern "C" hipError_t kvf_launch_partial_varlen_variant_timed(const char *id, const kvf_args_t *a,
+                                                              const kvf_varlen_args_t *va,
+                                                              hipStream_t st, hipEvent_t start,
+                                                              hipEvent_t stop) {
+  if (!a) return hipErrorInvalidValue;
+  const LaunchXFn fx = extended(id);
+  if (!fx) return hipErrorNotFound;
+  if (!a->part_o || !a->part_ml || !start || !stop) return hipErrorInvalidValue;
+  Launch l;
+  l.partial_only = true;
+  l.ev_start = start;
+  l.ev_stop = stop;
+  return fx(*a, ext_of(va), l, st);
+}
+
 extern "C" hipError_t kvf_launch_merge(int d, const kvf_args_t *a, hipStream_t st) {
   if (!a || a->splits < 1 || a->B < 1 || a->H < 1 || !a->part_o || !a->part_ml || !a->out)
     return hipErrorInvalidValue;

@@ -268,6 +268,34 @@ void kvfo_reference_attention_mt(int B, int H, int Hkv, int D, int n,
   for (auto &t : pool) t.join();
 }
 
+// kvfo_reference_attention_varlen over `threads` host threads (same output).
+void kvfo_reference_attention_varlen_mt(int B, int H, int Hkv, int D, int n_max,
+                                        const int32_t *lens, const float *q,
+                                        const float *K, const float *V, float scale,
+                                        float *out, int threads) {
+  const int gq = H / Hkv;
+  const int pairs = B * H;
+  if (threads < 1) threads = 1;
+  if (threads > pairs) threads = pairs;
+  auto work = [&](int w) {
+    std::vector<double> sc(n_max > 0 ? n_max : 1), acc(D);
+    for (int i = w; i < pairs; i += threads) {
+      const int b = i / H, h = i % H, hk = h / gq;
+      float *o = out + (long long)i * D;
+      if (lens[b] <= 0) {
+        std::fill(o, o + D, 0.f);
+        continue;
+      }
+      const long long base = ((long long)b * Hkv + hk) * n_max * D;
+      attend_one(D, lens[b], q + (long long)i * D, K + base, V + base, scale, o, sc, acc);
+    }
+  };
+  std::vector<std::thread> pool;
+  for (int w = 1; w < threads; ++w) pool.emplace_back(work, w);
+  work(0);
+  for (auto &t : pool) t.join();
+}
+
 void kvfo_reference_attention_varlen(int B, int H, int Hkv, int D, int n_max,
                                      const int32_t *lens, const float *q,
                                      const float *K, const float *V,

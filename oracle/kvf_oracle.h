@@ -89,6 +89,11 @@ void kvfo_reference_attention(int B, int H, int Hkv, int D, int n,
 void kvfo_reference_attention_mt(int B, int H, int Hkv, int D, int n,
                                  const float *q, const float *K, const float *V,
                                  float scale, float *out, int threads);
+/* As kvfo_reference_attention_varlen, over `threads` host threads. */
+void kvfo_reference_attention_varlen_mt(int B, int H, int Hkv, int D, int n_max,
+                                        const int32_t *lens, const float *q,
+                                        const float *K, const float *V, float scale,
+                                        float *out, int threads);
 void kvfo_reference_attention_varlen(int B, int H, int Hkv, int D, int n_max,
                                      const int32_t *lens, const float *q,
                                      const float *K, const float *V,

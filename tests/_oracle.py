@@ -57,6 +57,7 @@ def lib():
         "kvfo_reference_attention": (None, [_i, _i, _i, _i, _i, _p, _p, _p, _f, _p]),
         "kvfo_reference_attention_varlen": (None, [_i, _i, _i, _i, _i, _p, _p, _p, _p, _f, _p]),
         "kvfo_reference_attention_mt": (None, [_i, _i, _i, _i, _i, _p, _p, _p, _f, _p, _i]),
+        "kvfo_reference_attention_varlen_mt": (None, [_i, _i, _i, _i, _i, _p, _p, _p, _p, _f, _p, _i]),
         "kvfo_rel_l2": (_d, [_p, _p, _ll]),
         "kvfo_scale_log2": (_f, [_i]),
         "kvfo_reference_partials": (None, [_i, _i, _i, _i, _i, _i, _p, _p, _p, _f, _p, _p, _p]),
@@ -199,6 +200,22 @@ def reference_attention_varlen(q, K, V, lens, scale=None):
                                           _ptr(np.ascontiguousarray(q)),
                                           _ptr(np.ascontiguousarray(K)),
                                           _ptr(np.ascontiguousarray(V)), scale, _ptr(out))
+    return out
+
+
+def reference_attention_varlen_mt(q, K, V, lens, threads, scale=None):
+    """reference_attention_varlen over host threads; identical output."""
+    B, H, D = q.shape
+    _, Hkv, n_max, _ = K.shape
+    if scale is None:
+        scale = float(np.float32(1.0) / np.sqrt(np.float32(D)))
+    lens = np.ascontiguousarray(lens, dtype=np.int32)
+    out = np.empty((B, H, D), dtype=np.float32)
+    lib().kvfo_reference_attention_varlen_mt(B, H, Hkv, D, n_max, _ptr(lens),
+                                             _ptr(np.ascontiguousarray(q)),
+                                             _ptr(np.ascontiguousarray(K)),
+                                             _ptr(np.ascontiguousarray(V)), scale, _ptr(out),
+                                             threads)
     return out
 
 

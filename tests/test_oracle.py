@@ -242,6 +242,10 @@ def test_attention_threaded_is_identical():
     one = O.reference_attention(q, K, V)
     for threads in (1, 3, 8, 64):
         assert np.array_equal(O.reference_attention_mt(q, K, V, threads), one)
+    lens = np.array([257, 0], dtype=np.int32)
+    one = O.reference_attention_varlen(q, K, V, lens)
+    for threads in (1, 5, 64):
+        assert np.array_equal(O.reference_attention_varlen_mt(q, K, V, lens, threads), one)
 
 
 def test_attention_closed_forms():
