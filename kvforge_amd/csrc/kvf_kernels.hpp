@@ -30,7 +30,10 @@
 // query), V codes as operand B (MFMA k = the 32 tokens of the tile). The V
 // scale of a token and group is folded into that row's weight and the zero
 // point into a per-row running sum, so V is never dequantised element by
-// element; each lane keeps the rows whose group matches its V dims.
+// element; each lane keeps the rows whose group matches its V dims. Where hi
+// and lo halves share the MFMA (separate accumulator rows), the lo half
+// enters scaled by 2^11: a weight folded with a small V scale would otherwise
+// leave its lo half in the binary16 subnormal range and keep ~12 bits.
 //
 // Streaming: every wave keeps a ring of DEPTH tiles; tile k+DEPTH-1 is
 // issued before tile k is consumed. Loads are raw buffer loads through
@@ -74,6 +77,8 @@ constexpr int SUB = 16;                  // tokens per sub-tile (MFMA rows)
 constexpr int TT = 32;                   // tokens per tile (PV MFMA k)
 constexpr float TAU = 8.0f;              // rescale threshold, log2 units
 constexpr float CODE_SCALE = 16777216.f; // 2^24: undoes the subnormal encoding
+constexpr float LO_SCALE = 2048.f;       // 2^11: lo half of a packed softmax weight
+constexpr float LO_INV = 1.f / 2048.f;
 constexpr int RSRC_WORD3 = 0x00020000;   // gfx9 raw buffer: 32-bit data format
 constexpr int CPOL_NT = 2;               // nontemporal: every byte is used once
 
@@ -618,10 +623,15 @@ decode_partial(const Args a, const Ext x, const int final_out) {
         }
         w = col_live ? w : 0.f;
         const _Float16 hi = (_Float16)w;
-        const _Float16 lo = (_Float16)(w - (float)hi);
         if constexpr (HL) {
+          // the lo half has its own accumulator rows, so it enters scaled by
+          // 2^11 (it never exceeds the hi half, so this cannot overflow) and
+          // stays out of the binary16 subnormal range; the rows are scaled
+          // back where the wave's result is combined
+          const _Float16 lo = (_Float16)((w - (float)hi) * LO_SCALE);
           pa[p][0][i] = col_lo ? lo : hi;
         } else {
+          const _Float16 lo = (_Float16)(w - (float)hi);
           pa[p][0][i] = hi;
           pa[p][NQ - 1][i] = lo;
         }
@@ -720,7 +730,7 @@ decode_partial(const Args a, const Ext x, const int final_out) {
 #pragma unroll
     for (int e = 0; e < EV; ++e)
 #pragma unroll
-      for (int i = 0; i < 4; ++i) acc[0][e][i] += xor32(acc[0][e][i]);
+      for (int i = 0; i < 4; ++i) acc[0][e][i] = fmaf(xor32(acc[0][e][i]), LO_INV, acc[0][e][i]);
   }
 #pragma unroll
   for (int p = 0; p < PASSES; ++p)
@@ -734,7 +744,9 @@ decode_partial(const Args a, const Ext x, const int final_out) {
         float *dst = (lo_half ? sL : sO) + (wave * G + pr % G) * D + c * EV;
 #pragma unroll
         for (int e = 0; e < EV; ++e)
-          dst[e] = QUANT ? fmaf(acc[p][e][i], CODE_SCALE, lo_half ? 0.f : zrow[p][i]) : acc[p][e][i];
+          dst[e] = QUANT ? fmaf(acc[p][e][i], lo_half ? CODE_SCALE * LO_INV : CODE_SCALE,
+                                lo_half ? 0.f : zrow[p][i])
+                         : acc[p][e][i] * (lo_half ? LO_INV : 1.f);
       }
     }
   __syncthreads();
