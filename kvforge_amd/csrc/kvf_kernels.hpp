@@ -325,9 +325,13 @@ decode_partial(const Args a, const Ext x, const int final_out) {
   load_pages(0);
 
   // ---- issue all loads of wave-tile k into buf ---------------------------------
+  // Order: both sub-tiles' K, then the (scale, zero) words, then V. Wait counts
+  // are in issue order, so a wave can compute a tile's scores and softmax while
+  // its V is still arriving.
   auto issue = [&](Buf &buf, int k) __attribute__((always_inline)) {
     const bool live = k >= 0 && k < nk;
     const int tbase = (tile_first + wave + nw * k) * TT;
+    __amdgpu_buffer_rsrc_t rk[2], rv[2], rkm[2], rvm[2];
 #pragma unroll
     for (int s = 0; s < 2; ++s) {
       const int ts = tbase + s * SUB;
@@ -346,32 +350,41 @@ decode_partial(const Args a, const Ext x, const int final_out) {
       // tokens this sub-tile may read: up to the sequence end
       const int nv = live ? min(SUB, max(0, len - ts)) : 0;
       const uint32_t dbytes = nv > 0 ? (uint32_t)((nv - 1) * tstride * ROW + ROW) : 0u;
-      const auto rk = rsrc(a.k, row0 * ROW, dbytes);
-      const auto rv = rsrc(a.v, row0 * ROW, dbytes);
-#pragma unroll
-      for (int j = 0; j < NCH; ++j) bload<CH>(rk, koff + j * 4 * CH, buf.k[s][j]);
-#pragma unroll
-      for (int i = 0; i < 4; ++i) bload<VB>(rv, voff[i], buf.v[4 * s + i]);
+      rk[s] = rsrc(a.k, row0 * ROW, dbytes);
+      rv[s] = rsrc(a.v, row0 * ROW, dbytes);
       if constexpr (QUANT) {
         const uint32_t mbytes = nv > 0 ? (uint32_t)(((nv - 1) * tstride + 1) * NG * 4) : 0u;
-        const auto rkm = rsrc(a.k_meta, row0 * NG * 4, mbytes);
-        const auto rvm = rsrc(a.v_meta, row0 * NG * 4, mbytes);
+        rkm[s] = rsrc(a.k_meta, row0 * NG * 4, mbytes);
+        rvm[s] = rsrc(a.v_meta, row0 * NG * 4, mbytes);
+      }
+    }
+#pragma unroll
+    for (int s = 0; s < 2; ++s)
+#pragma unroll
+      for (int j = 0; j < NCH; ++j) bload<CH>(rk[s], koff + j * 4 * CH, buf.k[s][j]);
+    if constexpr (QUANT) {
+#pragma unroll
+      for (int s = 0; s < 2; ++s) {
         if constexpr (QMETA) {
-          bload<NG * 4>(rkm, mrow, buf.kmr[s]);
-          bload<NG * 4>(rvm, mrow, buf.vmr[s]);
+          bload<NG * 4>(rkm[s], mrow, buf.kmr[s]);
+          bload<NG * 4>(rvm[s], mrow, buf.vmr[s]);
         } else
 #pragma unroll
         for (int p = 0; p < PASSES; ++p)
 #pragma unroll
           for (int i = 0; i < 4; ++i) {
             Raw<4> t;
-            bload<4>(rkm, moff[p][i], t);
+            bload<4>(rkm[s], moff[p][i], t);
             buf.km[p][4 * s + i] = t.w[0];
-            bload<4>(rvm, moff[p][i], t);
+            bload<4>(rvm[s], moff[p][i], t);
             buf.vm[p][4 * s + i] = t.w[0];
           }
       }
     }
+#pragma unroll
+    for (int s = 0; s < 2; ++s)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) bload<VB>(rv[s], voff[i], buf.v[4 * s + i]);
   };
 
   // ---- query loads, then the first DEPTH-1 tiles under them ------------------------
