@@ -249,8 +249,11 @@ __device__ __forceinline__ int tau(int r, int i) { return (i >> 2) * SUB + 4 * r
 
 template <int D, int NT>
 __device__ void merge_head(const Args &a, const Ext &x, long long head, float *lds);
+// Split weights of the fused merge sit in LDS rows of merge_pad(S) floats.
+__host__ __device__ constexpr int merge_pad(int S) { return (S + 63) & ~63; }
+constexpr int CPOL_SC1 = 16; // buffer-load cache policy: device-coherent (sc1)
 template <int D, int G, int NT>
-__device__ void merge_group(const Args &a, const Ext &x, long long head0, float *lds);
+__device__ __forceinline__ void merge_group(const Args &a, const Ext &x, long long head0, float *lds);
 
 template <int FMT, int D, int GQ, int G, int U, int ORD, bool PAGED, int WPB>
 __global__ void __launch_bounds__(WPB * 64)
@@ -723,7 +726,7 @@ decode_partial(const Args a, const Ext x, const int final_out) {
     for (int i = 0; i < 4; ++i) zrow[p][i] = __shfl(z, 16 * r + ((4 * r + i) & 15));
   }
 
-  extern __shared__ float smem[];
+  extern __shared__ __attribute__((aligned(16))) float smem[]; // 16 B: the fused merge reads float4
   // layout: sO[nw][G][D], sM[nw][G][3], then (HL_LDS) sL[nw][G][D]
   float *sO = smem;
   float *sM = smem + nw * G * D;
@@ -823,11 +826,11 @@ decode_partial(const Args a, const Ext x, const int final_out) {
 
   // ---- fused merge: the last workgroup of a head group combines the splits ----
   // Every partial of this workgroup was written with an agent-scope atomic
-  // store, which completes at the device-coherent level; waiting for the
-  // stores to complete orders them before this workgroup's arrival on the
+  // store, which writes through to the device-coherent level; waiting for
+  // the stores to complete orders them before this workgroup's arrival on the
   // counter, so no L2 writeback (the agent-scope release fence) is needed.
   // The workgroup that arrives last reads every partial of its head group
-  // with agent-scope atomic loads, which are served from that level too.
+  // with device-coherent (sc1) loads, which are served from that level too.
   if (!final_out && x.counters) {
     __shared__ unsigned s_last;
     unsigned *cnt = x.counters + (long long)b * gridDim.y + hb;
@@ -846,80 +849,118 @@ decode_partial(const Args a, const Ext x, const int final_out) {
 }
 
 // Fused-step merge of the G heads [head0, head0 + G) by the last workgroup
-// of their head group: the same log-sum-exp recombination as decode_merge,
-// with every partial read through agent-scope atomic loads. Thread t owns
-// output elements t, t + NT, ...; it issues the loads of a chunk of splits
-// for all of them while the split maxima and sums of every head are loaded
-// into LDS, so a chunk costs one memory round trip. `lds` holds 2*G*S + G
-// floats.
+// of their head group: the same log-sum-exp recombination as decode_merge.
+// Partials are read with device-coherent (sc1) raw buffer loads, one
+// descriptor per head row, so a split past the end of its head's row reads
+// zero (the split offset goes into the vector offset, which the range check
+// covers; the scalar offset is not range-checked). Thread t owns output
+// elements t, t + NT, ... (EPT of them; with G*D < NT the waves past G*D
+// idle). The split maxima and sums and the first MC splits of its output
+// elements are all loaded before any is used, so up to MC splits cost one
+// memory round trip. The code is short and straight-line because it runs
+// once per head group from a cold instruction cache: the split weights sit
+// in LDS rows padded with zeros to merge_pad(S), so a chunk needs neither
+// bounds checks nor branches. `lds` holds 2*G*merge_pad(S) + G floats.
 template <int D, int G, int NT>
-__device__ void merge_group(const Args &a, const Ext &x, long long head0, float *lds) {
-  constexpr int EPT = (G * D + NT - 1) / NT;   // output elements per thread
-  constexpr int MC = EPT >= 4 ? 8 : 32 / EPT;  // splits per chunk
-  const int S = a.splits, tid = threadIdx.x;
-  float *sm = lds, *sl = lds + G * S, *sL = lds + 2 * G * S;
-  auto ld = [](const float *p) __attribute__((always_inline)) {
-    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+__device__ __forceinline__ void merge_group(const Args &a, const Ext &x, long long head0, float *lds) {
+  constexpr int CPOL = CPOL_SC1;
+  constexpr int EPT = G * D >= NT ? G * D / NT : 1; // output elements per thread
+  constexpr int MC = 64 / EPT;                      // splits per round trip
+  static_assert(G * D < NT ? NT % (G * D) == 0 : (G * D) % NT == 0, "merge geometry");
+  static_assert(D % 64 == 0, "a wave's output elements share one head");
+  const int S = a.splits, SP = merge_pad(S), tid = threadIdx.x;
+  float *sw = lds, *sl = lds + G * SP, *sL = lds + 2 * G * SP;
+  const bool active = G * D >= NT || tid < G * D; // wave-uniform
+  __amdgpu_buffer_rsrc_t ro[EPT];
+  int vo[EPT], hw[EPT];
+#pragma unroll
+  for (int e = 0; e < EPT; ++e) {
+    const int el = active ? tid + e * NT : 0;
+    hw[e] = el / D;
+    ro[e] = rsrc(a.part_o, head0 * S * D * 4, (uint32_t)((hw[e] + 1) * S * D * 4));
+    vo[e] = (hw[e] * S * D + el % D) * 4;
+  }
+  float o[EPT][MC];
+  auto load_chunk = [&](int s0) __attribute__((always_inline)) {
+#pragma unroll
+    for (int i = 0; i < MC; ++i)
+#pragma unroll
+      for (int e = 0; e < EPT; ++e)
+        o[e][i] = __builtin_bit_cast(
+            float, __builtin_amdgcn_raw_buffer_load_b32(ro[e], vo[e] + (s0 + i) * D * 4, 0, CPOL));
   };
-  for (int i = tid; i < G * S; i += NT) {
-    const float *ml = a.part_ml + ((head0 + i / S) * S + i % S) * 2;
-    sm[i] = ld(ml);
-    sl[i] = ld(ml + 1);
+  // (m, l) of (head t / SP, split t % SP): one pair per thread in flight with
+  // the first chunk; padding entries get m = -inf, l = 0 (a load past the
+  // descriptor's end returns zeros)
+  const __amdgpu_buffer_rsrc_t rml = rsrc(a.part_ml, head0 * S * 8, (uint32_t)(G * S * 8));
+  auto ml_off = [&](int t) __attribute__((always_inline)) {
+    const int s = t % SP;
+    return s < S ? ((t / SP) * S + s) * 8 : G * S * 8;
+  };
+  const i32x2_t ml0 = __builtin_amdgcn_raw_buffer_load_b64(rml, ml_off(tid), 0, CPOL);
+  if (active) load_chunk(0);
+  for (int t = tid; t < G * SP; t += NT) {
+    const i32x2_t ml = t == tid ? ml0 : __builtin_amdgcn_raw_buffer_load_b64(rml, ml_off(t), 0, CPOL);
+    // (elements go through plain ints: clang's __builtin_bit_cast of an
+    // ext_vector element reads element 0 whichever element is named)
+    const int mw = ml.x, lw = ml.y;
+    sw[t] = t % SP < S ? __builtin_bit_cast(float, mw) : -INFINITY;
+    sl[t] = __builtin_bit_cast(float, lw);
   }
   __syncthreads();
-  // per head: max, split weights (in place of the maxima) and the sum
+  // per head (one wave each): max, split weights in place of the maxima and
+  // the sum. Every lane walks the head's padded row itself, four entries per
+  // LDS read (broadcast reads, no cross-lane reduction).
   for (int h = tid >> 6; h < G; h += NT / 64) {
     const int lane = tid & 63;
+    const float4_t *w4 = reinterpret_cast<const float4_t *>(sw + h * SP);
+    const float4_t *l4 = reinterpret_cast<const float4_t *>(sl + h * SP);
     float M = -INFINITY;
-    for (int s = lane; s < S; s += 64) M = fmaxf(M, sm[h * S + s]);
-#pragma unroll
-    for (int m = 1; m < 64; m <<= 1) M = fmaxf(M, __shfl_xor(M, m));
-    float L = 0.f;
-    for (int s = lane; s < S; s += 64) {
-      const float ms = sm[h * S + s];
-      const float w = ms == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(ms - M);
-      sm[h * S + s] = w;
-      L = fmaf(sl[h * S + s], w, L);
+    for (int j = 0; j < SP / 4; ++j) {
+      const float4_t v = w4[j];
+      M = fmaxf(M, fmaxf(fmaxf(v[0], v[1]), fmaxf(v[2], v[3])));
     }
-#pragma unroll
-    for (int m = 1; m < 64; m <<= 1) L += __shfl_xor(L, m);
+    for (int s = lane; s < SP; s += 64) {
+      const float ms = sw[h * SP + s];
+      sw[h * SP + s] = ms == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(ms - M);
+    }
+    // the weights were stored as float and are read back as float4: keep the
+    // compiler from moving those reads above the stores (LDS operations of
+    // one wave complete in order)
+    asm volatile("" ::: "memory");
+    float L = 0.f;
+    for (int j = 0; j < SP / 4; ++j) {
+      const float4_t w = w4[j], l = l4[j];
+      L = fmaf(l[0], w[0], fmaf(l[1], w[1], fmaf(l[2], w[2], fmaf(l[3], w[3], L))));
+    }
     if (lane == 0) sL[h] = L;
   }
   __syncthreads();
+  if (!active) return;
   float O[EPT];
 #pragma unroll
   for (int e = 0; e < EPT; ++e) O[e] = 0.f;
   for (int s0 = 0; s0 < S; s0 += MC) {
-    float o[EPT][MC];
+    if (s0 > 0) load_chunk(s0);
 #pragma unroll
     for (int e = 0; e < EPT; ++e) {
-      const int el = tid + e * NT;
+      const float4_t *w4 = reinterpret_cast<const float4_t *>(sw + hw[e] * SP + s0);
 #pragma unroll
-      for (int i = 0; i < MC; ++i) {
-        const int s = s0 + i;
-        o[e][i] = (el < G * D && s < S)
-                      ? ld(a.part_o + ((head0 + el / D) * S + s) * D + el % D) : 0.f;
+      for (int i = 0; i < MC / 4; ++i) {
+        const float4_t w = w4[i];
+#pragma unroll
+        for (int k = 0; k < 4; ++k) O[e] = fmaf(o[e][4 * i + k], w[k], O[e]);
       }
-    }
-#pragma unroll
-    for (int e = 0; e < EPT; ++e) {
-      const int el = tid + e * NT;
-      const int h = el < G * D ? el / D : 0;
-#pragma unroll
-      for (int i = 0; i < MC; ++i)
-        if (s0 + i < S) O[e] = fmaf(o[e][i], sm[h * S + s0 + i], O[e]);
     }
   }
 #pragma unroll
   for (int e = 0; e < EPT; ++e) {
     const int el = tid + e * NT;
-    if (el < G * D) {
-      const float L = sL[el / D];
-      const float res = L > 0.f ? O[e] / L : 0.f;
-      const long long head = head0 + el / D;
-      if (x.out16) x.out16[head * D + el % D] = (_Float16)res;
-      else a.out[head * D + el % D] = res;
-    }
+    const float L = sL[hw[e]];
+    const float res = L > 0.f ? O[e] / L : 0.f;
+    const long long head = head0 + hw[e];
+    if (x.out16) x.out16[head * D + el % D] = (_Float16)res;
+    else a.out[head * D + el % D] = res;
   }
 }
 
@@ -1014,11 +1055,11 @@ hipError_t launch_group(const Args &a, const Ext &x, const Launch &l, hipStream_
   // LDS; beyond 64 KiB of them the step runs as two launches (the counters
   // are then left untouched, at zero)
   const bool fused = x.counters && !final_out && !l.partial_only &&
-                     (size_t)(2 * G * a.splits + G) * sizeof(float) <= 65536;
+                     (size_t)(2 * G * merge_pad(a.splits) + G) * sizeof(float) <= 65536;
   Ext xk = x;
   if (!fused) xk.counters = nullptr;
   size_t lds = combine_lds<FMT, D, GQ, G>(a.warps);
-  if (fused) lds = std::max(lds, (size_t)(2 * G * a.splits + G) * sizeof(float));
+  if (fused) lds = std::max(lds, (size_t)(2 * G * merge_pad(a.splits) + G) * sizeof(float));
   auto kernel = a.warps == 4 ? &decode_partial<FMT, D, GQ, G, U, ORD, PAGED, 4>
                              : &decode_partial<FMT, D, GQ, G, U, ORD, PAGED, 8>;
   if (l.ev_start || l.ev_stop)
