@@ -247,8 +247,6 @@ template <int N, int I = 0, class F> __device__ __forceinline__ void static_for(
 // layouts: sub-tile i/4, row 4r + i%4.
 __device__ __forceinline__ int tau(int r, int i) { return (i >> 2) * SUB + 4 * r + (i & 3); }
 
-template <int D, int NT>
-__device__ void merge_head(const Args &a, const Ext &x, long long head, float *lds);
 // Split weights of the fused merge sit in LDS rows of merge_pad(S) floats.
 __host__ __device__ constexpr int merge_pad(int S) { return (S + 63) & ~63; }
 constexpr int CPOL_SC1 = 16; // buffer-load cache policy: device-coherent (sc1)
@@ -964,85 +962,58 @@ __device__ __forceinline__ void merge_group(const Args &a, const Ext &x, long lo
   }
 }
 
-// Log-sum-exp recombination of the split partials of one head by one
-// workgroup of NT lanes (runtime/kvf_kernels.cuh:288-306 computes the same
-// with one thread per dim walking the splits; empty splits, m = -inf, are
-// skipped there and here). Lane (slice, d) with slice = tid / D sums splits
-// slice, slice + NT/D, ...: all of its partial-output loads are issued at
-// once, while wave 0 loads the split maxima and sums, finds the head's max
-// and writes the split weights to LDS, so a head costs one memory round
-// trip. `lds` holds S + NT floats.
-constexpr int MERGE_CHUNK = 16; // splits per lane per round trip
+// Stand-alone merge: one workgroup of D threads per (query head, sequence),
+// thread d owning output dim d. It is the log-sum-exp recombination of
+// runtime/kvf_kernels.cuh:288-306: M = max of the split maxima, empty splits
+// (m = -inf) skipped, out = sum_s O_s 2^(m_s - M) / sum_s l_s 2^(m_s - M), 0
+// when the sum is 0. Every thread loads the (m, l) pairs itself (all lanes
+// read the same address) beside its MERGE_CHUNK partial outputs, so up to
+// MERGE_CHUNK splits cost one memory round trip and need no LDS and no
+// barrier; beyond that, chunks are folded with a running max. Loads go
+// through buffer descriptors over the head's rows: a split past the end reads
+// zero and is masked to m = -inf without a branch.
+constexpr int MERGE_CHUNK = 32;
 
-template <int D, int NT>
-__device__ void merge_head(const Args &a, const Ext &x, long long head, float *lds) {
-  constexpr int SL = NT / D;
-  static_assert(SL >= 1 && NT % D == 0, "merge geometry");
-  const int S = a.splits;
-  const int tid = threadIdx.x, d = tid % D, sl = tid / D;
-  const float *ml = a.part_ml + head * S * 2;
-  const float *po = a.part_o + head * S * D + d;
-  float *sw = lds;          // [S] split weights
-  float *red = lds + S;     // [NT] slice sums, then the head's L
-  float O = 0.f;
-  for (int s0 = 0; s0 < S; s0 += SL * MERGE_CHUNK) {
-    float o[MERGE_CHUNK];
-#pragma unroll
-    for (int i = 0; i < MERGE_CHUNK; ++i) {
-      const int s = s0 + sl + i * SL;
-      o[i] = s < S ? po[(long long)s * D] : 0.f;
-    }
-    if (s0 == 0 && tid < 64) {
-      float M = -INFINITY;
-      for (int s = tid; s < S; s += 64) M = fmaxf(M, ml[2 * s]);
-#pragma unroll
-      for (int m = 1; m < 64; m <<= 1) M = fmaxf(M, __shfl_xor(M, m));
-      float L = 0.f;
-      for (int s = tid; s < S; s += 64) {
-        const float ms = ml[2 * s];
-        const float w = ms == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(ms - M);
-        sw[s] = w;
-        L = fmaf(ml[2 * s + 1], w, L);
-      }
-#pragma unroll
-      for (int m = 1; m < 64; m <<= 1) L += __shfl_xor(L, m);
-      if (tid == 0) red[NT - 1] = L;
-    }
-    __syncthreads();
-#pragma unroll
-    for (int i = 0; i < MERGE_CHUNK; ++i) {
-      const int s = s0 + sl + i * SL;
-      if (s < S) O = fmaf(o[i], sw[s], O);
-    }
-  }
-  const float L = red[NT - 1];
-  __syncthreads();
-  red[tid] = O;
-  __syncthreads();
-  if (tid < D) {
-    float o = 0.f;
-#pragma unroll
-    for (int i = 0; i < SL; ++i) o += red[i * D + tid];
-    const float res = L > 0.f ? o / L : 0.f;
-    if (x.out16) x.out16[head * D + tid] = (_Float16)res;
-    else a.out[head * D + tid] = res;
-  }
-  __syncthreads(); // lds is reused by the next head
-}
-
-constexpr int MERGE_THREADS = 512;
-
-// Stand-alone merge: one workgroup per (query head, sequence).
 template <int D>
-__global__ void __launch_bounds__(MERGE_THREADS) decode_merge(const Args a, const Ext x) {
-  extern __shared__ float lds[];
-  merge_head<D, MERGE_THREADS>(a, x, (long long)blockIdx.y * a.H + blockIdx.x, lds);
+__global__ void __launch_bounds__(D) decode_merge(const Args a, const Ext x) {
+  const long long head = (long long)blockIdx.y * a.H + blockIdx.x;
+  const int S = a.splits, d = threadIdx.x;
+  const __amdgpu_buffer_rsrc_t rml = rsrc(a.part_ml, head * S * 8, (uint32_t)(S * 8));
+  const __amdgpu_buffer_rsrc_t ro = rsrc(a.part_o, head * S * D * 4, (uint32_t)(S * D * 4));
+  float M = -INFINITY, L = 0.f, O = 0.f;
+  for (int s0 = 0; s0 < S; s0 += MERGE_CHUNK) {
+    float m[MERGE_CHUNK], l[MERGE_CHUNK], o[MERGE_CHUNK];
+#pragma unroll
+    for (int i = 0; i < MERGE_CHUNK; ++i) {
+      const i32x2_t p = __builtin_amdgcn_raw_buffer_load_b64(rml, (s0 + i) * 8, 0, 0);
+      const int pm = p.x, pl = p.y; // (element-wise: see the fused merge)
+      m[i] = s0 + i < S ? __builtin_bit_cast(float, pm) : -INFINITY;
+      l[i] = __builtin_bit_cast(float, pl);
+      o[i] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(ro, ((s0 + i) * D + d) * 4, 0, 0));
+    }
+    float Mc = M;
+#pragma unroll
+    for (int i = 0; i < MERGE_CHUNK; ++i) Mc = fmaxf(Mc, m[i]);
+    if (Mc == -INFINITY) continue; // every split so far is empty
+    const float alpha = M == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(M - Mc);
+    L *= alpha;
+    O *= alpha;
+#pragma unroll
+    for (int i = 0; i < MERGE_CHUNK; ++i) {
+      const float w = m[i] == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m[i] - Mc);
+      L = fmaf(l[i], w, L);
+      O = fmaf(o[i], w, O);
+    }
+    M = Mc;
+  }
+  const float res = L > 0.f ? O / L : 0.f;
+  if (x.out16) x.out16[head * D + d] = (_Float16)res;
+  else a.out[head * D + d] = res;
 }
 
 template <int D>
 inline hipError_t launch_merge_kernel(const Args &a, const Ext &x, hipStream_t st) {
-  hipLaunchKernelGGL((decode_merge<D>), dim3(a.H, a.B), dim3(MERGE_THREADS),
-                     (size_t)(a.splits + MERGE_THREADS) * sizeof(float), st, a, x);
+  hipLaunchKernelGGL((decode_merge<D>), dim3(a.H, a.B), dim3(D), 0, st, a, x);
   return hipGetLastError();
 }
 
@@ -1085,7 +1056,6 @@ inline bool args_ok(const Args &a, int fmt, int D, int G, bool paged) {
     const int gq = 1 << a.group_shift;
     if (a.group_shift < 5 || a.group_shift > 7 || gq > D) return false;
   }
-  if ((size_t)(a.splits + 512) * sizeof(float) > 60 * 1024) return false; // merge weights in LDS
   if (paged && (a.block_shift < 4 || a.block_shift > 12 || !a.block_table || a.max_blocks < 1))
     return false;
   return true;
