@@ -54,7 +54,7 @@ METRIC = ("\u00b5s/decode step + achieved HBM GB/s (% of peak), "
           "GQA32/8 d128 32k int8:64")
 CONFIG_DEFAULTS = {  # config -> (fmt, group, n, order, block tokens, splits)
     2: ("int8", 64, 32768, "hm", 0, 32),
-    3: ("int8", 64, 8192, "tm", 16, 16),
+    3: ("int8", 64, 8192, "tm", 16, 8),
     4: ("int4", 32, 65536, "hm", 0, 32),
 }
 
