@@ -139,6 +139,18 @@ def test_empty_splits_and_partials():
     check(b, out.cpu().numpy(), "merge")
 
 
+def test_merge_split_counts():
+    # the merge folds the splits 32 at a time with a running max: split counts
+    # around and past one chunk, for both head dimensions, and one where the
+    # last splits own no token
+    for D, n in ((128, 3000), (64, 2500)):
+        b = build(Case(2, 8, 2, D, n, R.FMT_INT8, 32, R.ORD_HEAD, 0, seed=11))
+        for splits in (31, 33, 97):
+            check(b, run(b, splits), f"D={D} S={splits}")
+    b = build(Case(1, 4, 4, 128, 150, R.FMT_F16, 0, R.ORD_HEAD, 0, seed=12))
+    check(b, run(b, 100, pack=False), "n=150 S=100")
+
+
 def test_north_star_int8_32k():
     # GQA 32/8, d128, n32768, int8:64 with 1% outlier
     # channels x8, head-major contiguous, splits swept
