@@ -52,10 +52,10 @@ sys.path.insert(0, ROOT)
 HBM_PEAK_GBS = 8000.0
 METRIC = ("\u00b5s/decode step + achieved HBM GB/s (% of peak), "
           "GQA32/8 d128 32k int8:64")
-CONFIG_DEFAULTS = {  # config -> (fmt, group, n, order, block tokens, splits)
-    2: ("int8", 64, 32768, "hm", 0, 32),
-    3: ("int8", 64, 8192, "tm", 16, 8),
-    4: ("int4", 32, 65536, "hm", 0, 32),
+CONFIG_DEFAULTS = {  # config -> (fmt, group, n, order, block tokens, splits, waves)
+    2: ("int8", 64, 32768, "hm", 0, 32, 4),
+    3: ("int8", 64, 8192, "tm", 16, 8, 4),
+    4: ("int4", 32, 65536, "hm", 0, 32, 8),
 }
 
 
@@ -72,7 +72,7 @@ def parse():
     p.add_argument("--order", default=None, choices=["hm", "tm"])
     p.add_argument("--block-tokens", type=int, default=None)
     p.add_argument("--splits", type=int, default=None)
-    p.add_argument("--warps", type=int, default=4)
+    p.add_argument("--warps", type=int, default=None, help="wavefronts per workgroup (4 or 8)")
     p.add_argument("--unroll", type=int, default=2)
     p.add_argument("--pack", type=int, default=1)
     p.add_argument("--copies", type=int, default=0,
@@ -84,7 +84,8 @@ def parse():
                         "two-launch kvf_launch_variant")
     p.add_argument("--json-only", action="store_true")
     a = p.parse_args()
-    fmt, group, n, order, bt, splits = CONFIG_DEFAULTS[a.config]
+    fmt, group, n, order, bt, splits, waves = CONFIG_DEFAULTS[a.config]
+    a.warps = a.warps or waves
     a.fmt = a.fmt or fmt
     a.group = a.group if a.group is not None else group
     a.n = a.n or n

@@ -15,12 +15,18 @@
 //   output  the reference's sweep CSV columns.
 // MI355X specifics: the cache is quantized and placed on the GPU by the
 // library's own kvf_quantize_place (bit-exact with the reference's host
-// quantizer); the flush writes 512 MiB, twice the 256 MiB MALL, so no rep
+// quantizer); the flush reads 512 MiB, twice the 256 MiB MALL, so no rep
 // finds the cache in the memory-side cache; `warps` are 64-lane wavefronts.
+// The reference flushes by writing (a memset). On MI355X that leaves the
+// MALL full of dirty lines, and a plan whose loads allocate there pays for
+// their write-back (token-major plans measured 1.6x slower after a 512 MiB
+// memset than after a 512 MiB read); reading evicts the cache just as well
+// and leaves the memory system as a decode step finds it after the
+// preceding layers. `--flush write` restores the reference's memset.
 //
 //   kvf_sweep --plans a.csv[,b.csv] --out sweep.csv
 //             [--reps 25] [--warmup 5] [--seed 1] [--limit N] [--device 0]
-//             [--threads T]
+//             [--threads T] [--flush read|write]
 #include "kvf_abi.h"
 
 #include <hip/hip_runtime.h>
@@ -218,6 +224,13 @@ struct DeviceCache {
   }
 };
 
+// Reads n 16-byte words once: evicts the memory-side cache without dirtying it.
+__global__ void __launch_bounds__(256) flush_read(const uint4 *p, size_t n, unsigned *sink) {
+  unsigned acc = 0;
+  for (size_t i = (size_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (size_t)gridDim.x * 256) acc ^= p[i].x ^ p[i].w;
+  if (acc == 0x9e3779b9u) sink[threadIdx.x] = acc; // keeps the loads; practically never taken
+}
+
 } // namespace
 
 int main(int argc, char **argv) {
@@ -225,6 +238,7 @@ int main(int argc, char **argv) {
   int reps = 25, warmup = 5, limit = 0, dev = 0;
   int threads = static_cast<int>(std::min(16u, std::max(1u, std::thread::hardware_concurrency())));
   uint64_t seed = 1;
+  bool flush_by_write = false;
   for (int i = 1; i < argc; ++i) {
     const std::string a = argv[i];
     auto next = [&]() -> std::string {
@@ -242,6 +256,14 @@ int main(int argc, char **argv) {
     else if (a == "--seed") seed = std::stoull(next());
     else if (a == "--device") dev = std::stoi(next());
     else if (a == "--threads") threads = std::max(1, std::stoi(next()));
+    else if (a == "--flush") {
+      const std::string f = next();
+      if (f != "read" && f != "write") {
+        std::fprintf(stderr, "--flush takes read or write\n");
+        return 2;
+      }
+      flush_by_write = f == "write";
+    }
     else {
       std::fprintf(stderr, "unknown option %s\n", a.c_str());
       return 2;
@@ -260,10 +282,13 @@ int main(int argc, char **argv) {
               prop.multiProcessorCount, threads);
   std::printf("registry: %d variants\n", kvf_variant_count());
 
-  // 512 MiB flush region: twice the MALL, written before every timed rep
+  // 512 MiB flush region: twice the MALL, read (or written) before every timed rep
   const size_t flush_bytes = 512ull << 20;
   void *flush = nullptr;
+  unsigned *flush_sink = nullptr;
   CHECK(hipMalloc(&flush, flush_bytes));
+  CHECK(hipMalloc(&flush_sink, 256 * sizeof(unsigned)));
+  CHECK(hipMemset(flush, 0, flush_bytes));
   hipStream_t st;
   CHECK(hipStreamCreate(&st));
   hipEvent_t e0, e1;
@@ -416,7 +441,13 @@ int main(int argc, char **argv) {
 
         std::vector<float> ms;
         for (int r = 0; r < warmup + reps; ++r) {
-          CHECK(hipMemsetAsync(flush, r & 0xff, flush_bytes, st));
+          if (flush_by_write) {
+            CHECK(hipMemsetAsync(flush, r & 0xff, flush_bytes, st));
+          } else {
+            hipLaunchKernelGGL(flush_read, dim3(4096), dim3(256), 0, st, static_cast<const uint4 *>(flush),
+                               flush_bytes / 16, flush_sink);
+            CHECK(hipGetLastError());
+          }
           CHECK(hipEventRecord(e0, st));
           CHECK(kvf_launch_variant(vid.c_str(), &a, st));
           CHECK(hipEventRecord(e1, st));
@@ -451,6 +482,7 @@ int main(int argc, char **argv) {
   }
   std::fclose(out);
   CHECK(hipFree(flush));
+  CHECK(hipFree(flush_sink));
   std::printf("\ndone: %lld timed, %lld skipped, %lld failed verification\nwrote %s\n", done, skipped, unverified,
               out_path.c_str());
   return unverified ? 3 : 0;
