@@ -22,7 +22,9 @@
 //
 // Quantized codes enter the MFMAs as binary16 subnormals (code * 2^-24),
 // built by one v_perm per two codes; gfx950 MFMAs keep subnormal inputs, so
-// the products are exact. Scores of quantized formats are kept in units of
+// the products are exact. int4 high nibbles are masked in place (code * 16,
+// still subnormal): the query slots they meet carry 1/16 and the V dims they
+// fill are scaled back with the code scale. Scores of quantized formats are kept in units of
 // 2^-24 and the factor is folded into the exp2 argument.
 //
 // PV: one 16x16x32 MFMA per 16 output dims and tile, the softmax weights as
@@ -79,6 +81,7 @@ constexpr float TAU = 8.0f;              // rescale threshold, log2 units
 constexpr float CODE_SCALE = 16777216.f; // 2^24: undoes the subnormal encoding
 constexpr float LO_SCALE = 2048.f;       // 2^11: lo half of a packed softmax weight
 constexpr float LO_INV = 1.f / 2048.f;
+constexpr float INT4_HI = 16.f;          // high nibbles enter the MFMAs as code * 16
 constexpr int RSRC_WORD3 = 0x00020000;   // gfx9 raw buffer: 32-bit data format
 constexpr int CPOL_NT = 2;               // nontemporal: every byte is used once
 // Cache policy of the K/V payload loads. Head-major rows stream as
@@ -88,6 +91,12 @@ constexpr int CPOL_NT = 2;               // nontemporal: every byte is used once
 // took 18.9 us against 16.4 us, and the KV head whose rows sit at byte 384
 // of every 1 KiB token block lagged the others by ~4.5 us.
 template <int ORD> constexpr int cpol_kv() { return ORD == ORD_TOKEN ? 0 : CPOL_NT; }
+
+// Factor that undoes the code * 16 of int4 high nibbles (odd dims of a
+// lane's V block) in the PV accumulators.
+template <int FMT> __device__ constexpr float vdim_scale(int e) {
+  return FMT == FMT_INT4 && (e & 1) ? 1.f / INT4_HI : 1.f;
+}
 
 template <int FMT> constexpr int bits_of() {
   return FMT == FMT_F16 ? 16 : FMT == FMT_INT8 ? 8 : 4;
@@ -457,8 +466,10 @@ decode_partial(const Args a, const Ext x, const int final_out) {
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
           const float v = mine ? raw[ks][slot_elem<FMT>(i)] * a.scale_log2 : 0.f;
-          const _Float16 hi = (_Float16)v;
-          const _Float16 lo = (_Float16)(v - (float)hi);
+          // int4: slots 4-7 meet high nibbles entered as code * 16
+          const float vb = FMT == FMT_INT4 && i >= 4 ? v * (1.f / INT4_HI) : v;
+          const _Float16 hi = (_Float16)vb;
+          const _Float16 lo = (_Float16)(vb - (float)hi);
           if constexpr (HL) {
             qb[p][0][ks][i] = col_lo ? lo : hi;
           } else {
@@ -564,8 +575,10 @@ decode_partial(const Args a, const Ext x, const int final_out) {
             aw[2] = perm(0u, w1, 0x0c010c00u);
             aw[3] = perm(0u, w1, 0x0c030c02u);
           } else {
+            // high nibbles stay in place (code * 16): the query slots they
+            // meet carry 1/16, which saves the shift
             const uint32_t w = buf.k[st][j].w[m];
-            const uint32_t lo = w & 0x0F0F0F0Fu, hi = (w >> 4) & 0x0F0F0F0Fu;
+            const uint32_t lo = w & 0x0F0F0F0Fu, hi = w & 0xF0F0F0F0u;
             aw[0] = perm(0u, lo, 0x0c010c00u);
             aw[1] = perm(0u, lo, 0x0c030c02u);
             aw[2] = perm(0u, hi, 0x0c010c00u);
@@ -671,9 +684,11 @@ decode_partial(const Args a, const Ext x, const int final_out) {
         } else if constexpr (FMT == FMT_INT8) {
           bw[q2] = perm(tb.w[e / 4], ta.w[e / 4], sel_pair(e & 3));
         } else {
-          const int sh = (e & 1) * 4;
-          const uint32_t na = (ta.w[0] >> sh) & 0x0F0F0F0Fu;
-          const uint32_t nb = (tb.w[0] >> sh) & 0x0F0F0F0Fu;
+          // odd dims (high nibbles) stay in place: code * 16, undone with
+          // the code scale at the wave's result
+          const uint32_t msk = (e & 1) ? 0xF0F0F0F0u : 0x0F0F0F0Fu;
+          const uint32_t na = ta.w[0] & msk;
+          const uint32_t nb = tb.w[0] & msk;
           bw[q2] = perm(nb, na, sel_pair((e >> 1) & 3));
         }
       }
@@ -765,7 +780,7 @@ decode_partial(const Args a, const Ext x, const int final_out) {
         float *dst = (lo_half ? sL : sO) + (wave * G + pr % G) * D + c * EV;
 #pragma unroll
         for (int e = 0; e < EV; ++e)
-          dst[e] = QUANT ? fmaf(acc[p][e][i], lo_half ? CODE_SCALE * LO_INV : CODE_SCALE,
+          dst[e] = QUANT ? fmaf(acc[p][e][i], (lo_half ? CODE_SCALE * LO_INV : CODE_SCALE) * vdim_scale<FMT>(e),
                                 lo_half ? 0.f : zrow[p][i])
                          : acc[p][e][i] * (lo_half ? LO_INV : 1.f);
       }
