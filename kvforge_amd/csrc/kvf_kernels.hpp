@@ -43,8 +43,11 @@
 // stops the loads at the sequence end, and a tile outside the wave's range
 // gets zero-length descriptors whose loads return zeros without touching
 // memory, so the load stream is unconditional and the compiler's wait counts
-// are static. The first DEPTH-1 tiles are issued before the query is
-// converted, so the two latencies overlap.
+// are static. Within a tile both sub-tiles' K go first, then the (scale,
+// zero) words, then V, so scores and softmax start before V has arrived.
+// The first DEPTH-1 tiles are issued before the query is converted, so the
+// two latencies overlap. Head-major rows load as nontemporal; token-major
+// rows use the default cache policy (see cpol_kv).
 //
 // Online softmax keeps one running max per head for the whole wave and only
 // rescales when a score exceeds it by more than TAU (log2 units): a
