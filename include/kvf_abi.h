@@ -160,6 +160,21 @@ hipError_t kvf_quantize_place(int fmt, int group, int d, const float *x,
                               int max_blocks, unsigned char *data, void *meta,
                               hipStream_t stream);
 
+/* Append one token per sequence: quantize the B*Hkv rows of `x`
+ * ([B][Hkv][d] fp32, device memory) and write row (b, h) to token
+ * positions[b] (device int32 [B]) of the same layouts as kvf_quantize_place,
+ * whose arithmetic it shares, so appending every token of a cache one call
+ * at a time produces the same bytes as placing it whole. A position outside
+ * [0, n) (contiguous) or [0, max_blocks*block_tokens) (paged) writes nothing.
+ * No counterpart in the reference, which quantizes on the host
+ * (runtime/kvf_host.h:72-121); it is the per-step form of that step. */
+hipError_t kvf_append_tokens(int fmt, int group, int d, const float *x,
+                             int B, int Hkv, int n, const int *positions,
+                             int order, int block_tokens,
+                             const int *block_table, int max_blocks,
+                             unsigned char *data, void *meta,
+                             hipStream_t stream);
+
 /* Library version string. */
 const char *kvf_version(void);
 

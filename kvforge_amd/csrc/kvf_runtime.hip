@@ -6,7 +6,7 @@
 //       kvf::Registry;
 //   kvf_launch_merge
 //       the log-sum-exp merge alone;
-//   kvf_quantize_place
+//   kvf_quantize_place, kvf_append_tokens
 //       the KV append step: quantize fp32 rows on the GPU and scatter them to
 //       their physical rows, bit-exact with runtime/kvf_host.h:72-135,166-184.
 #include "kvf_kernels.hpp"
@@ -57,13 +57,24 @@ template <int FMT>
 __global__ void __launch_bounds__(256)
 quantize_place_kernel(const float *__restrict__ x, long long rows, int d, int group, int Hkv,
                       int n, int order, int bt, const int *table, int max_blocks,
-                      unsigned char *data, uint32_t *meta) {
+                      unsigned char *data, uint32_t *meta, const int *positions) {
   const int lane = threadIdx.x & 63;
   const long long row = (long long)blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
   if (row >= rows) return; // whole wavefronts leave together
-  const int t = (int)(row % n);
-  const int h = (int)((row / n) % Hkv);
-  const int b = (int)(row / ((long long)n * Hkv));
+  // bulk: row r is token r % n of head (r / n) % Hkv of sequence r / (n Hkv);
+  // append: row r is head r % Hkv of sequence r / Hkv at token positions[b],
+  // and a position outside the layout writes nothing
+  int t, h, b;
+  if (positions) {
+    h = (int)(row % Hkv);
+    b = (int)(row / Hkv);
+    t = positions[b];
+    if (t < 0 || t >= (bt ? max_blocks * bt : n)) return;
+  } else {
+    t = (int)(row % n);
+    h = (int)((row / n) % Hkv);
+    b = (int)(row / ((long long)n * Hkv));
+  }
   long long prow;
   if (bt == 0) {
     prow = order == ORD_HEAD ? ((long long)b * Hkv + h) * n + t : ((long long)b * n + t) * Hkv + h;
@@ -219,10 +230,11 @@ extern "C" const char *kvf_variant_id(int i) {
   return (i >= 0 && i < (int)ids.size()) ? ids[i].c_str() : nullptr;
 }
 
-extern "C" hipError_t kvf_quantize_place(int fmt, int group, int d, const float *x, int B,
-                                         int Hkv, int n, int order, int block_tokens,
-                                         const int *block_table, int max_blocks,
-                                         unsigned char *data, void *meta, hipStream_t st) {
+namespace {
+hipError_t quantize_rows(int fmt, int group, int d, const float *x, int B, int Hkv, int n,
+                         const int *positions, int order, int block_tokens,
+                         const int *block_table, int max_blocks, unsigned char *data,
+                         void *meta, hipStream_t st) {
   if (!x || !data || B < 1 || Hkv < 1 || n < 1 || (d != 64 && d != 128)) return hipErrorInvalidValue;
   if (order != ORD_HEAD && order != ORD_TOKEN) return hipErrorInvalidValue;
   if (block_tokens < 0 || (block_tokens > 0 && (!block_table || max_blocks * block_tokens < n)))
@@ -230,27 +242,46 @@ extern "C" hipError_t kvf_quantize_place(int fmt, int group, int d, const float 
   if (fmt != FMT_F16) {
     if (!meta || (group != 32 && group != 64 && group != 128) || group > d) return hipErrorInvalidValue;
   }
-  const long long rows = (long long)B * Hkv * n;
+  const long long rows = (long long)B * Hkv * (positions ? 1 : n);
   const dim3 block(256);
   const dim3 grid((unsigned)((rows + 3) / 4));
   uint32_t *m = static_cast<uint32_t *>(meta);
   switch (fmt) {
   case FMT_F16:
     hipLaunchKernelGGL(quantize_place_kernel<FMT_F16>, grid, block, 0, st, x, rows, d, group, Hkv,
-                       n, order, block_tokens, block_table, max_blocks, data, m);
+                       n, order, block_tokens, block_table, max_blocks, data, m, positions);
     break;
   case FMT_INT8:
     hipLaunchKernelGGL(quantize_place_kernel<FMT_INT8>, grid, block, 0, st, x, rows, d, group,
-                       Hkv, n, order, block_tokens, block_table, max_blocks, data, m);
+                       Hkv, n, order, block_tokens, block_table, max_blocks, data, m, positions);
     break;
   case FMT_INT4:
     hipLaunchKernelGGL(quantize_place_kernel<FMT_INT4>, grid, block, 0, st, x, rows, d, group,
-                       Hkv, n, order, block_tokens, block_table, max_blocks, data, m);
+                       Hkv, n, order, block_tokens, block_table, max_blocks, data, m, positions);
     break;
   default:
     return hipErrorInvalidValue;
   }
   return hipGetLastError();
+}
+} // namespace
+
+extern "C" hipError_t kvf_quantize_place(int fmt, int group, int d, const float *x, int B,
+                                         int Hkv, int n, int order, int block_tokens,
+                                         const int *block_table, int max_blocks,
+                                         unsigned char *data, void *meta, hipStream_t st) {
+  return quantize_rows(fmt, group, d, x, B, Hkv, n, nullptr, order, block_tokens, block_table,
+                       max_blocks, data, meta, st);
+}
+
+extern "C" hipError_t kvf_append_tokens(int fmt, int group, int d, const float *x, int B, int Hkv,
+                                        int n, const int *positions, int order,
+                                        int block_tokens, const int *block_table,
+                                        int max_blocks, unsigned char *data, void *meta,
+                                        hipStream_t st) {
+  if (!positions) return hipErrorInvalidValue;
+  return quantize_rows(fmt, group, d, x, B, Hkv, n, positions, order, block_tokens, block_table,
+                       max_blocks, data, meta, st);
 }
 
 extern "C" const char *kvf_version(void) { return "kvforge-mi355x 0.1 (gfx950)"; }

@@ -86,6 +86,8 @@ def hip_lib():
     L.kvf_variant_id.argtypes = [I]
     L.kvf_quantize_place.restype = I
     L.kvf_quantize_place.argtypes = [I, I, I, P, I, I, I, I, I, P, I, P, P, P]
+    L.kvf_append_tokens.restype = I
+    L.kvf_append_tokens.argtypes = [I, I, I, P, I, I, I, P, I, I, P, I, P, P, P]
     L.kvf_version.restype = ctypes.c_char_p
     L.kvf_version.argtypes = []
     _hip = L
@@ -211,6 +213,16 @@ def quantize_place(fmt, group, d, x, B, Hkv, n, order, block_tokens, table, max_
         fmt, group, d, _ptr(x), B, Hkv, n, order, block_tokens, _ptr(table), max_blocks,
         _ptr(data), _ptr(meta), stream_handle(stream))
     check(err, "kvf_quantize_place")
+
+
+def append_tokens(fmt, group, d, x, B, Hkv, n, positions, order, block_tokens, table,
+                  max_blocks, data, meta, stream=None):
+    """GPU KV append of one token per sequence: x [B][Hkv][d] fp32 rows go to
+    token positions[b] of each sequence, quantized exactly as quantize_place."""
+    err = hip_lib().kvf_append_tokens(
+        fmt, group, d, _ptr(x), B, Hkv, n, _ptr(positions), order, block_tokens, _ptr(table),
+        max_blocks, _ptr(data), _ptr(meta), stream_handle(stream))
+    check(err, "kvf_append_tokens")
 
 
 def row_bytes(fmt, d):

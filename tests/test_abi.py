@@ -30,7 +30,7 @@ def _c_functions(path):
 
 def test_header_declares_entry_points():
     names = _c_functions(os.path.join(INCLUDE, "kvf_abi.h"))
-    for must in ("kvf_launch_variant", "kvf_launch_merge", "kvf_quantize_place",
+    for must in ("kvf_launch_variant", "kvf_launch_merge", "kvf_quantize_place", "kvf_append_tokens",
                  "kvf_variant_count", "kvf_variant_id"):
         assert must in names
     assert len(names) == len(set(names))

@@ -282,3 +282,36 @@ def test_every_registered_variant(fmt, group, order, bt, D):
             assert vid(b, G > 1, U) in ids
             splits, warps = ((1, 8), (5, 4))[i] if G % 2 == 0 else ((3, 4), (1, 8))[i]
             check(b, run(b, splits, pack=G > 1, unroll=U, warps=warps), f"G={G} U={U} S={splits} W={warps}")
+
+
+@pytest.mark.parametrize("fmt,group,order,bt", [
+    (R.FMT_INT8, 64, R.ORD_HEAD, 0), (R.FMT_INT4, 32, R.ORD_TOKEN, 0),
+    (R.FMT_INT8, 128, R.ORD_TOKEN, 16), (R.FMT_F16, 0, R.ORD_HEAD, 64)])
+def test_append_tokens_equals_whole_cache_placement(fmt, group, order, bt):
+    # appending a cache one token per sequence and step, each sequence at its
+    # own position, gives the bytes the oracle's quantize + place give for the
+    # whole cache; a position past the layout writes nothing
+    B, Hkv, D, n = 3, 2, 128, 40
+    _, K, _ = O.make_data(B, 2 * Hkv, Hkv, D, n, 21)
+    kd, km, _ = O.quantize(fmt, group, D, K)
+    pkd, pkm, table, mb = O.place(B, Hkv, n, fmt, group, D, order, bt, kd, km)
+    dev = torch.device("cuda:0")
+    rows, _ = R.rows_alloc(B, Hkv, n, bt)
+    mw = D // group if fmt != R.FMT_F16 else 0
+    data = torch.zeros(rows * R.row_bytes(fmt, D), dtype=torch.uint8, device=dev)
+    meta = torch.zeros(rows * mw, dtype=torch.int32, device=dev) if mw else None
+    tbl = torch.from_numpy(table.astype(np.int32)).to(dev) if bt else None
+    Kt = torch.from_numpy(K.reshape(B, Hkv, n, D))
+    offs = [0, 7, 23]
+    for step in range(n + 1):
+        # the last step's positions all lie outside the layout, which holds
+        # max_blocks * block_tokens tokens per sequence when paged
+        past = mb * bt if bt else n
+        pos = [(step + o) % n for o in offs] if step < n else [past, -1, 1 << 20]
+        x = Kt[torch.arange(B), :, torch.tensor([min(p, n - 1) for p in pos])].contiguous().to(dev)
+        pt = torch.tensor(pos, dtype=torch.int32, device=dev)
+        R.append_tokens(fmt, group, D, x, B, Hkv, n, pt, order, bt, tbl, mb, data, meta)
+    torch.cuda.synchronize()
+    assert np.array_equal(data.cpu().numpy(), pkd.ravel()), "codes differ"
+    if mw:
+        assert np.array_equal(meta.cpu().numpy().view(np.uint32), pkm.ravel()), "meta differs"
