@@ -988,7 +988,8 @@ __device__ __forceinline__ void merge_group(const Args &a, const Ext &x, long lo
 }
 
 // Stand-alone merge: one workgroup of D threads per (query head, sequence),
-// thread d owning output dim d. It is the log-sum-exp recombination of
+// thread d owning output dim d. Its arguments are six scalars (10 dwords)
+// rather than Args, so all of them can arrive preloaded in SGPRs. It is the log-sum-exp recombination of
 // runtime/kvf_kernels.cuh:288-306: M = max of the split maxima, empty splits
 // (m = -inf) skipped, out = sum_s O_s 2^(m_s - M) / sum_s l_s 2^(m_s - M), 0
 // when the sum is 0. Every thread loads the (m, l) pairs itself (all lanes
@@ -1000,11 +1001,12 @@ __device__ __forceinline__ void merge_group(const Args &a, const Ext &x, long lo
 constexpr int MERGE_CHUNK = 32;
 
 template <int D>
-__global__ void __launch_bounds__(D) decode_merge(const Args a, const Ext x) {
-  const long long head = (long long)blockIdx.y * a.H + blockIdx.x;
-  const int S = a.splits, d = threadIdx.x;
-  const __amdgpu_buffer_rsrc_t rml = rsrc(a.part_ml, head * S * 8, (uint32_t)(S * 8));
-  const __amdgpu_buffer_rsrc_t ro = rsrc(a.part_o, head * S * D * 4, (uint32_t)(S * D * 4));
+__global__ void __launch_bounds__(D)
+decode_merge(const float *part_o, const float *part_ml, float *out, _Float16 *out16, int H, int S) {
+  const long long head = (long long)blockIdx.y * H + blockIdx.x;
+  const int d = threadIdx.x;
+  const __amdgpu_buffer_rsrc_t rml = rsrc(part_ml, head * S * 8, (uint32_t)(S * 8));
+  const __amdgpu_buffer_rsrc_t ro = rsrc(part_o, head * S * D * 4, (uint32_t)(S * D * 4));
   float M = -INFINITY, L = 0.f, O = 0.f;
   for (int s0 = 0; s0 < S; s0 += MERGE_CHUNK) {
     float m[MERGE_CHUNK], l[MERGE_CHUNK], o[MERGE_CHUNK];
@@ -1032,15 +1034,16 @@ __global__ void __launch_bounds__(D) decode_merge(const Args a, const Ext x) {
     M = Mc;
   }
   const float res = L > 0.f ? O / L : 0.f;
-  if (x.out16) x.out16[head * D + d] = (_Float16)res;
-  else a.out[head * D + d] = res;
+  if (out16) out16[head * D + d] = (_Float16)res;
+  else out[head * D + d] = res;
 }
 
-template <int D>
-inline hipError_t launch_merge_kernel(const Args &a, const Ext &x, hipStream_t st) {
-  hipLaunchKernelGGL((decode_merge<D>), dim3(a.H, a.B), dim3(D), 0, st, a, x);
-  return hipGetLastError();
-}
+// Launches decode_merge<D>. Defined and instantiated (D = 64, 128) in
+// kvf_merge.hip alone, which is built with its six arguments preloaded into
+// SGPRs, so the merge starts its loads without a kernel-argument round trip.
+template <int D> hipError_t launch_merge_kernel(const Args &a, const Ext &x, hipStream_t st);
+extern template hipError_t launch_merge_kernel<64>(const Args &, const Ext &, hipStream_t);
+extern template hipError_t launch_merge_kernel<128>(const Args &, const Ext &, hipStream_t);
 
 template <int FMT, int D, int GQ, int G, int U, int ORD, bool PAGED>
 hipError_t launch_group(const Args &a, const Ext &x, const Launch &l, hipStream_t st) {
