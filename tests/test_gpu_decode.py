@@ -226,6 +226,48 @@ def test_varlen_pool_f16_qo():
         assert err < REL_TOL
 
 
+VARLEN_CASES = [
+    # (B, H, Hkv, D, n, fmt, group, order, bt, lengths, splits)
+    (5, 8, 2, 128, 700, R.FMT_F16, 0, R.ORD_HEAD, 0, [0, 1, 33, 700, 64], (2, 3, 8, 40)),
+    (9, 8, 2, 128, 900, R.FMT_INT8, 64, R.ORD_TOKEN, 16, [900] + [1] * 7 + [32], (2, 3)),
+    (3, 8, 2, 64, 300, R.FMT_INT4, 32, R.ORD_HEAD, 32, [0, 0, 0], (4,)),
+    (1, 32, 8, 128, 3000, R.FMT_INT8, 64, R.ORD_HEAD, 0, [2999], (2, 7, 64)),
+    (64, 4, 2, 64, 200, R.FMT_INT8, 32, R.ORD_TOKEN, 0, "random", (2, 5)),
+    (65, 4, 1, 64, 120, R.FMT_INT4, 64, R.ORD_TOKEN, 16, "random", (3,)),
+]
+
+
+@pytest.mark.parametrize("case", VARLEN_CASES, ids=lambda c: f"B{c[0]}_{R.FMT_NAMES[c[5]]}")
+def test_varlen_edge_lengths(case):
+    # per-sequence lengths: empty and one-token sequences, lengths at and
+    # around a tile, one long sequence beside many short ones, a batch of
+    # empty sequences, batches of 64 and 65, and tokens past each length
+    # that must not be read. The partial buffers start as NaN, so a merge
+    # that read a slot no workgroup wrote would show.
+    B, H, Hkv, D, n, fmt, group, order, bt, lens, split_list = case
+    if isinstance(lens, str):
+        rng = np.random.default_rng(B)
+        lens = rng.integers(0, n + 1, size=B)
+        lens[::7] = 0
+        lens[1] = n
+    lens = np.asarray(lens, dtype=np.int32)
+    b = build(Case(B, H, Hkv, D, n, fmt, group, order, bt, seed=21))
+    ref = O.reference_attention_varlen(b.q_host, b.kdeq, b.vdeq, lens)
+    lens_d = torch.from_numpy(lens).to("cuda:0")
+    for splits in split_list:
+        for pack, unroll, warps in ((True, 2, 4), (False, 4, 8)):
+            b.out.fill_(float("nan"))
+            a = args(b, splits, warps)
+            R.launch_varlen(vid(b, pack, unroll), a, lens_d)
+            torch.cuda.synchronize()
+            got = b.out.cpu().numpy()
+            err = O.rel_l2(got, ref) if np.any(ref) else float(np.max(np.abs(got)))
+            say(f"  {b.case.tag()} lens {lens.min()}..{lens.max()} S={splits} pack={pack}: err={err:.3g}")
+            assert np.all(np.isfinite(got))
+            assert np.all(got[lens == 0] == 0)
+            assert err < REL_TOL
+
+
 def test_bad_arguments_are_rejected():
     b = build(Case(1, 8, 2, 128, 64, R.FMT_INT8, 64, R.ORD_HEAD, 0), check_cache=False)
     a = args(b, 1, 4)
