@@ -606,8 +606,10 @@ Cost warpEvaluate(const DecodeSpec &s, const Machine &m, const Calib &c, const P
 //   GQA        unpacked query heads re-read their KV head; the re-reads hit L2
 //              with probability unpack_l2_hit * window and go at bw_l2, the
 //              rest come from HBM again
-//   issue      VALU wave-instructions per tile (MFMA cycles / 4 folded in) at
-//              one wave-instruction per SIMD slot, waves per SIMD sharing it,
+//   issue      VALU wave-instructions and MFMA issue slots (cycles / 4) per
+//              tile at one per SIMD slot, waves per SIMD sharing it: their sum
+//              for a wave alone on its SIMD, the larger of the two once two or
+//              more waves share it (one's MFMAs run under another's VALU);
 //              spills (scratch bytes per lane) costing spill_cost per 64 B
 //   fixed      launch_frac and merge_frac (second kernel) of launch_us, plus
 //              warp_w0 loaded latencies per round of workgroups (query load,
@@ -616,7 +618,8 @@ Cost warpEvaluate(const DecodeSpec &s, const Machine &m, const Calib &c, const P
 struct CdnaTile {
   int depth = 2;     // ring of tiles per wave
   double bytes = 0;  // K + V + meta bytes of one tile
-  double instr = 0;  // wave-instructions per tile (VALU + MFMA cycles / 4)
+  double valu = 0;   // VALU wave-instructions per tile
+  double mfma = 0;   // MFMA issue slots per tile (cycles / 4)
 };
 
 CdnaTile cdnaTile(const DecodeSpec &s, const Plan &p, int G) {
@@ -634,7 +637,8 @@ CdnaTile cdnaTile(const DecodeSpec &s, const Plan &p, int G) {
   const double k_conv = p.fmt.fmt == Format::F16 ? 0.0 : p.fmt.fmt == Format::INT8 ? 0.5 : 0.875;
   const double v_conv = p.fmt.fmt == Format::INT4 ? 0.8 : 0.5;
   const double softmax = 8.0 * (p.fmt.isQuantized() ? 9.0 : 6.0) * passes;
-  t.instr = (k_conv + v_conv) * 32.0 * s.d / 64.0 + softmax + 24.0 + 16.0 * mfma / 4.0;
+  t.valu = (k_conv + v_conv) * 32.0 * s.d / 64.0 + softmax + 24.0;
+  t.mfma = 16.0 * mfma / 4.0;
   return t;
 }
 
@@ -704,11 +708,15 @@ Cost cdnaEvaluate(const DecodeSpec &s, const Machine &m, const Calib &c, const P
   const double l2 = m.bw_l2_gbs > 0 ? m.bw_l2_gbs : m.bw_peak_gbs;
   k.t_mem_us = rounds * (conc * wg_kv / (k.bw_eff_gbs * 1000.0) + conc * wg_l2 / (l2 * 1000.0));
 
-  // issue: tiles per wave, waves per SIMD sharing its slots
+  // issue: tiles per wave, waves per SIMD sharing its slots. A wave alone on
+  // its SIMD waits on its own MFMA chain between VALU sections; with two or
+  // more, the matrix core runs one wave's MFMAs while another issues VALU, so
+  // a tile costs the SIMD the larger of the two rather than their sum
   const double tiles_wave = std::ceil((std::ceil(chunk / 32.0) + 1.0) / waves);
   const double simd_waves = std::max(1.0, waves * per_cu / 4.0);
   const double simd_rate = m.fSmGflops() / 4.0 / 128.0; // wave-instructions per ns per SIMD
-  k.t_cmp_us = rounds * tiles_wave * t.instr * simd_waves * (1.0 + c.spill_cost * kr.scratch / 64.0) /
+  const double per_tile = simd_waves >= 2.0 ? std::max(t.valu, t.mfma) : t.valu + t.mfma;
+  k.t_cmp_us = rounds * tiles_wave * per_tile * simd_waves * (1.0 + c.spill_cost * kr.scratch / 64.0) /
                (simd_rate * std::max(1e-6, c.issue_eff)) / 1000.0;
   k.memory_bound = k.t_mem_us >= k.t_cmp_us;
   const double t_par =
