@@ -234,6 +234,31 @@ std::string kernelSource(const Module &m) {
   if (p.layout.paged()) o << "  a.block_shift = " << ilog2(p.layout.block_tokens) << ";\n";
   o << "  return kvf::launch" << templateArgs(p, s.g(), s.d) << "(a, st);\n";
   o << "}\n\n";
+  if (m.q16 || m.varlen) {
+    // the program's extension: per-sequence lengths and/or binary16 q/out,
+    // passed beside the unchanged Args (kvf_varlen_args_t, kvf_abi.h)
+    o << "// " << (m.varlen ? "per-sequence lengths (Args::n is the maximum)" : "one length for every sequence")
+      << ", " << (m.q16 ? "binary16" : "fp32") << " query and output\n";
+    o << "extern \"C\" hipError_t kvf_launch_varlen_" << s.name
+      << "(const kvf::Args *in, const kvf_varlen_args_t *va, hipStream_t st) {\n";
+    o << "  if (!in || !va) return hipErrorInvalidValue;\n";
+    if (m.varlen) o << "  if (!va->seq_lens) return hipErrorInvalidValue;\n";
+    if (m.q16) o << "  if (!va->q16 || !va->out16) return hipErrorInvalidValue;\n";
+    o << "  kvf::Args a = *in;\n";
+    o << "  a.splits = " << p.part.splits << ";\n";
+    o << "  a.warps = " << p.part.warps << ";\n";
+    if (p.fmt.isQuantized()) o << "  a.group_shift = " << ilog2(p.fmt.group) << ";\n";
+    if (p.layout.paged()) o << "  a.block_shift = " << ilog2(p.layout.block_tokens) << ";\n";
+    o << "  kvf::gfx950::Ext x;\n";
+    if (m.varlen) o << "  x.seq_lens = va->seq_lens;\n";
+    if (m.q16) {
+      o << "  x.q16 = static_cast<const _Float16 *>(va->q16);\n";
+      o << "  x.out16 = static_cast<_Float16 *>(va->out16);\n";
+    }
+    o << "  return kvf::gfx950::launch_ext" << templateArgs(p, s.g(), s.d)
+      << "(a, x, kvf::gfx950::Launch{}, st);\n";
+    o << "}\n\n";
+  }
   o << "extern \"C\" const char *kvf_plan_" << s.name << "() { return \"" << p.str() << "\"; }\n";
   return o.str();
 }
@@ -265,6 +290,11 @@ std::string planHeader(const Module &m) {
   std::ostringstream us;
   us << op.cost.t_total_us;
   def("KVF_PRED_US", us.str());
+  if (m.q16 || m.varlen) { // this build's extension only
+    def("KVF_LAUNCH_VARLEN", "kvf_launch_varlen_" + s.name);
+    def("KVF_SEQ_LENS", m.varlen ? "1" : "0");
+    def("KVF_Q_F16", m.q16 ? "1" : "0");
+  }
   return o.str();
 }
 

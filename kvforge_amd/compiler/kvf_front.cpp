@@ -86,7 +86,7 @@ namespace {
 // Words the language reserves; they cannot name a tensor or a key.
 const std::set<std::string> &reserved() {
   static const std::set<std::string> r{"target", "decode", "kvcache", "query", "decode_attn", "scale",
-                                       "auto",   "splits", "gqa_pack", "true", "false"};
+                                       "auto",   "splits", "gqa_pack", "true", "false", "seq_lens"};
   return r;
 }
 
@@ -337,8 +337,17 @@ private:
         } else {
           fail("expected true, false or '?'");
         }
+      } else if (isWord("seq_lens")) {
+        next();
+        punct('=');
+        if (isWord("true") || isWord("false")) {
+          a.seq_lens = isWord("true");
+          next();
+        } else {
+          fail("expected true or false");
+        }
       } else {
-        fail("expected scale=, splits= or gqa_pack=");
+        fail("expected scale=, splits=, gqa_pack= or seq_lens=");
       }
     }
     punct(')');
@@ -364,7 +373,7 @@ const Operation &Module::attn() const {
 std::string ValueTy::str() const {
   std::ostringstream o;
   if (!cache) {
-    o << "tensor<" << rows << "x" << cols << "xf32>";
+    o << "tensor<" << rows << "x" << cols << (f16 ? "xf16>" : "xf32>");
   } else {
     o << "kvcache<" << rows << "x" << cols << "x" << (fmt_free ? std::string("?") : fmt.str()) << ", "
       << (layout_free ? std::string("?/?") : layout.str()) << ">";
@@ -466,7 +475,12 @@ Module lowerSource(const SourceFile &sf) {
     throw std::runtime_error("decode_attn names an undeclared query '" + fn.attn.q + "'");
   if (fn.query.rows != "H" || fn.query.cols != "d")
     throw std::runtime_error("query must be declared as query<H, d, f32>");
-  if (fn.query.dtype != "f32") throw std::runtime_error("only f32 queries are supported");
+  // f16 (binary16 query and output) is this build's extension; the reference
+  // accepts f32 only (src/ir.cpp:144-145)
+  if (fn.query.dtype != "f32" && fn.query.dtype != "f16")
+    throw std::runtime_error("only f32 or f16 queries are supported");
+  m.q16 = fn.query.dtype == "f16";
+  m.varlen = fn.attn.seq_lens;
 
   bool kf_free = false, vf_free = false, kl_free = false, vl_free = false;
   const KvFormat kf = resolveFormat(*kd, s.d, kf_free);
@@ -494,6 +508,7 @@ Module lowerSource(const SourceFile &sf) {
   ValueTy dense;
   dense.rows = s.H;
   dense.cols = s.d;
+  dense.f16 = m.q16;
   auto defining = [](Op kind, int result) {
     Operation op;
     op.op = kind;
@@ -544,6 +559,7 @@ std::string printModule(const Module &m) {
     if (typed >= 0) o << " : " << m.values[typed].ty.str();
     if (op.op == Op::DecodeAttn || op.op == Op::DecodeAttnSplit) {
       o << " {scale = " << op.scale;
+      if (m.varlen) o << ", seq_lens = true";
       if (op.planned) {
         o << ", format = " << op.plan.fmt.str() << ", layout = " << op.plan.layout.str()
           << ", splits = " << op.plan.part.splits << ", gqa_pack = " << (op.plan.part.gqa_pack ? "true" : "false")

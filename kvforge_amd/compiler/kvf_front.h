@@ -78,6 +78,7 @@ struct AttnCall {
   double scale = 0;
   int splits = 0; // 0: free
   int gqa_pack = -1; // -1 free, 0 false, 1 true
+  bool seq_lens = false; // per-sequence lengths (extension; n is the maximum)
   int line = 1;
 };
 
@@ -109,6 +110,7 @@ struct ValueTy {
   KvFormat fmt;
   KvLayout layout;
   bool fmt_free = false, layout_free = false;
+  bool f16 = false; // binary16 dense tensor (query and output of an f16 query)
   std::string str() const;
 };
 
@@ -136,6 +138,10 @@ struct Module {
   std::vector<SsaValue> values;
   std::vector<Operation> ops;
   std::vector<Ranked> ranked; // every candidate, cheapest first
+  // extensions beside the reference's program (the emitted TU then also
+  // exports kvf_launch_varlen_<name>): binary16 query and output, and
+  // per-sequence lengths
+  bool q16 = false, varlen = false;
   int add(const std::string &name, const ValueTy &ty);
   const Operation &attn() const;
 };

@@ -206,6 +206,44 @@ def launch_varlen(vid, args, seq_lens, q16=None, out16=None, stream=None):
     check(err, f"kvf_launch_varlen_variant({vid})")
 
 
+_plans = {}
+
+
+def plan_lib(name):
+    """Load kvforge_amd/plans/libkvf_plan_<name>.so, the library `kvf plan`
+    emitted for plans/<name>.kv (kvf_launch_<name>, kvf_plan_<name>, and
+    kvf_launch_varlen_<name> when the program declares an f16 query or
+    seq_lens); raise if it is not built."""
+    if name in _plans:
+        return _plans[name]
+    path = os.path.join(HERE, "plans", f"libkvf_plan_{name}.so")
+    if not os.path.exists(path):
+        raise KvfError(f"{path} is missing: run __graft_entry__.build() (or make -C kvforge_amd) first")
+    hip_lib()  # the plan library links against it
+    L = ctypes.CDLL(path)
+    getattr(L, f"kvf_launch_{name}").restype = ctypes.c_int
+    getattr(L, f"kvf_launch_{name}").argtypes = [ctypes.POINTER(Args), ctypes.c_void_p]
+    getattr(L, f"kvf_plan_{name}").restype = ctypes.c_char_p
+    getattr(L, f"kvf_plan_{name}").argtypes = []
+    if hasattr(L, f"kvf_launch_varlen_{name}"):
+        fn = getattr(L, f"kvf_launch_varlen_{name}")
+        fn.restype = ctypes.c_int
+        fn.argtypes = [ctypes.POINTER(Args), ctypes.POINTER(VarlenArgs), ctypes.c_void_p]
+    _plans[name] = L
+    return L
+
+
+def launch_plan_varlen(name, args, seq_lens, q16=None, out16=None, stream=None):
+    """kvf_launch_varlen_<name> of a planned program's library."""
+    va = VarlenArgs()
+    va.seq_lens = seq_lens.data_ptr() if seq_lens is not None else None
+    va.q16 = q16.data_ptr() if q16 is not None else None
+    va.out16 = out16.data_ptr() if out16 is not None else None
+    err = getattr(plan_lib(name), f"kvf_launch_varlen_{name}")(ctypes.byref(args), ctypes.byref(va),
+                                                                stream_handle(stream))
+    check(err, f"kvf_launch_varlen_{name}")
+
+
 def quantize_place(fmt, group, d, x, B, Hkv, n, order, block_tokens, table, max_blocks,
                    data, meta, stream=None):
     """GPU KV append: fp32 logical rows -> codes + (scale, zero) in the layout."""

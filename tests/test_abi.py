@@ -78,3 +78,14 @@ def test_args_layout_matches_reference():
     assert a.B.offset == 9 * p
     assert a.scale_log2.offset == 9 * p + 9 * 4
     assert ctypes.sizeof(a) == 9 * p + 9 * 4 + 4
+
+
+def test_planned_program_library_exports_its_entry_points():
+    # kvforge_amd/plans/config3.kv, planned and built by `make -C kvforge_amd`:
+    # the reference's two entry points plus the variable-length one; the plan
+    # string is host data, readable without a GPU
+    L = R.plan_lib("config3")
+    for sym in ("kvf_launch_config3", "kvf_launch_varlen_config3", "kvf_plan_config3"):
+        assert hasattr(L, sym), sym
+    plan = L.kvf_plan_config3().decode()
+    assert plan.startswith("int8:64 | token_major/paged:16 | splits=8 pack w"), plan

@@ -285,3 +285,64 @@ def test_mi355x_model_top1_against_measured_sweep(tmp_path):
     ns8 = [ln for ln in text8.splitlines() if "H32_Hkv8_d128_n32768_b1" in ln][0]
     assert float(ns8.split("regret=")[1].split("%")[0]) < 1.0, ns8
     assert "splits=32 pack w4" in ns8, ns8
+
+
+# ------------------------------------- extension: f16 query and per-sequence lengths
+def _ext_program(dtype="f16", seq="true"):
+    return (f'target machine = "{os.path.join(ROOT, "machines", "mi355x.gpu")}"\n'
+            "decode pool(H: 32, H_kv: 8, d: 128, n: 8192, batch: 8) {\n"
+            f"  Q: query<H, d, {dtype}>\n"
+            "  K: kvcache<n, d, int8:64, token_major, paged:16>\n"
+            "  V: kvcache<n, d, int8:64, token_major, paged:16>\n"
+            f"  O = decode_attn(Q, K, V, scale = auto, splits = 8, gqa_pack = true, seq_lens = {seq})\n"
+            "}\n")
+
+
+def test_f16_query_and_seq_lens_emit_varlen_launcher(tmp_path):
+    r = kvf("plan", write(tmp_path, "pool.kv", _ext_program()), "--out", str(tmp_path / "o"))
+    assert r.returncode == 0, r.stderr
+    tu = (tmp_path / "o" / "decode_pool.hip").read_text()
+    assert ('extern "C" hipError_t kvf_launch_varlen_pool(const kvf::Args *in, '
+            'const kvf_varlen_args_t *va, hipStream_t st)') in tu
+    assert "if (!va->seq_lens) return hipErrorInvalidValue;" in tu
+    assert "if (!va->q16 || !va->out16) return hipErrorInvalidValue;" in tu
+    assert "x.seq_lens = va->seq_lens;" in tu and "x.out16 = static_cast<_Float16 *>(va->out16);" in tu
+    assert "kvf::gfx950::launch_ext<kvf::FMT_INT8, 128, 4, " in tu
+    # the reference's launcher stays, unchanged
+    assert 'extern "C" hipError_t kvf_launch_pool(const kvf::Args *in, hipStream_t st)' in tu
+    hdr = (tmp_path / "o" / "plan_info.h").read_text()
+    assert "#define KVF_LAUNCH_VARLEN kvf_launch_varlen_pool" in hdr
+    assert "#define KVF_SEQ_LENS 1" in hdr and "#define KVF_Q_F16 1" in hdr
+    ir = (tmp_path / "o" / "ir.txt").read_text()
+    assert "tensor<32x128xf16>" in ir and "seq_lens = true" in ir
+    # lengths alone keep the fp32 query: no binary16 checks, no q16/out16
+    r = kvf("plan", write(tmp_path, "p32.kv", _ext_program("f32")), "--out", str(tmp_path / "o32"))
+    assert r.returncode == 0, r.stderr
+    tu32 = (tmp_path / "o32" / "decode_pool.hip").read_text()
+    assert "kvf_launch_varlen_pool" in tu32 and "va->q16" not in tu32
+    # a program without the extension emits exactly the reference's entry points
+    r = kvf("plan", write(tmp_path, "plain.kv", _ext_program("f32", "false")), "--out", str(tmp_path / "op"))
+    assert r.returncode == 0, r.stderr
+    assert "varlen" not in (tmp_path / "op" / "decode_pool.hip").read_text()
+    assert "KVF_LAUNCH_VARLEN" not in (tmp_path / "op" / "plan_info.h").read_text()
+
+
+@pytest.mark.parametrize("text,needle", [
+    (_ext_program("bf16"), "only f32 or f16 queries"),
+    (_ext_program("f16", "maybe"), "expected true or false"),
+])
+def test_extension_rejections(tmp_path, text, needle):
+    r = kvf("plan", write(tmp_path, "bad.kv", text), "--out", str(tmp_path / "o"))
+    assert r.returncode != 0 and needle in r.stderr, r.stderr
+
+
+@pytest.mark.skipif(not os.path.exists(HIPCC), reason="hipcc not installed")
+def test_generated_varlen_launcher_compiles_for_gfx950(tmp_path):
+    r = kvf("plan", write(tmp_path, "pool.kv", _ext_program()), "--out", str(tmp_path / "o"))
+    assert r.returncode == 0, r.stderr
+    c = subprocess.run([HIPCC, "-std=c++17", "-O1", "--offload-arch=gfx950", "-c",
+                        "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+                        "-I", os.path.join(ROOT, "include"), "-I", os.path.join(ROOT, "kvforge_amd", "csrc"),
+                        str(tmp_path / "o" / "decode_pool.hip"), "-o", str(tmp_path / "pool.o")],
+                       capture_output=True, text=True)
+    assert c.returncode == 0, c.stderr[-2000:]

@@ -224,6 +224,20 @@ def test_varlen_pool_f16_qo():
         err = O.rel_l2(got, ref)
         say(f"  varlen S={splits}: rel_l2={err:.3g}")
         assert err < REL_TOL
+    # the same step through the library kvf planned from kvforge_amd/plans/config3.kv
+    # (its launcher fixes splits = 8 and the plan's waves and shifts)
+    plan = R.plan_lib("config3").kvf_plan_config3().decode()
+    assert plan.startswith("int8:64 | token_major/paged:16 | splits=8 pack"), plan
+    po = torch.full((B, H, 8, D), float("nan"), device=dev)
+    pm = torch.full((B, H, 8, 2), float("nan"), device=dev)
+    a = R.make_args(qdummy, kc, vc, kmc, vmc, tbl, outdummy, po, pm, B, H, Hkv, n_max,
+                    1, 8, group=64, block_tokens=16, max_blocks=mb, D=D)
+    out16.fill_(float("nan"))
+    R.launch_plan_varlen("config3", a, lens_d, q16=q16d, out16=out16)
+    torch.cuda.synchronize()
+    err = O.rel_l2(out16.float().cpu().numpy(), ref)
+    say(f"  planned config3 ({plan}): rel_l2={err:.3g}")
+    assert err < REL_TOL
 
 
 VARLEN_CASES = [
