@@ -827,22 +827,19 @@ decode_partial(const Args a, const Ext x, const int final_out) {
       if (x.out16) x.out16[head * D + col] = (_Float16)res;
       else a.out[head * D + col] = res;
     } else {
-      // fused step: agent-scope atomic stores (write-through to the level
-      // every XCD sees), published below without an L2 writeback
+      // agent-scope atomic stores: written through to the level every XCD
+      // sees while the kernel still runs, so the fused step publishes them
+      // without an L2 writeback, and in the two-launch step the writeback at
+      // the kernel's end has no partials left to flush before the merge
+      // (decode step, alternating rounds on two boxes: north star
+      // 18.2 -> 17.6 us and 18.0 -> 17.9 us, config 4 24.7 -> 24.2 us,
+      // config 3 27.8 -> 28.0 us; the split kernel alone 0.1 us longer)
       float *po = a.part_o + (head * a.splits + split) * D + col;
       float *pm = a.part_ml + (head * a.splits + split) * 2;
-      if (x.counters) {
-        __hip_atomic_store(po, O, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        if (col == 0) {
-          __hip_atomic_store(pm, M, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-          __hip_atomic_store(pm + 1, L, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        }
-      } else {
-        *po = O;
-        if (col == 0) {
-          pm[0] = M;
-          pm[1] = L;
-        }
+      __hip_atomic_store(po, O, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      if (col == 0) {
+        __hip_atomic_store(pm, M, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_store(pm + 1, L, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       }
     }
   }
