@@ -20,12 +20,16 @@
 // at most 8 columns the hi half sits in columns 0-7 and the lo half in 8-15,
 // so one MFMA yields both; otherwise hi and lo are two MFMAs.
 //
-// Quantized codes enter the MFMAs as binary16 subnormals (code * 2^-24),
-// built by one v_perm per two codes; gfx950 MFMAs keep subnormal inputs, so
-// the products are exact. int4 high nibbles are masked in place (code * 16,
-// still subnormal): the query slots they meet carry 1/16 and the V dims they
-// fill are scaled back with the code scale. Scores of quantized formats are kept in units of
-// 2^-24 and the factor is folded into the exp2 argument.
+// Quantized codes enter the MFMAs as exact binary16 values: one v_perm
+// (int8) or mask (int4) places two codes as subnormals code * 2^-24. K codes
+// stay in that form; V codes go on, through one packed binary16 fma, to
+// (code - mid) * 2^-10, centred on the format's mid-range and in the normal
+// range (PV products of subnormal codes measured less precise, and the
+// centring keeps sum p*code*scale and sum p*zero from cancelling; the zero
+// points absorb mid * scale). int4 high nibbles are masked in place (code *
+// 16): the query slots they meet carry 1/16 and the V dims they fill are
+// scaled back with the code scale. Scores of quantized formats are kept in
+// units of 2^-24 and the factor is folded into the exp2 argument.
 //
 // PV: one 16x16x32 MFMA per 16 output dims and tile, the softmax weights as
 // operand A (rows = the same (group, head) pairs, hi/lo split like the
@@ -86,10 +90,18 @@ typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
 constexpr int SUB = 16;                  // tokens per sub-tile (MFMA rows)
 constexpr int TT = 32;                   // tokens per tile (PV MFMA k)
 constexpr float TAU = 8.0f;              // rescale threshold, log2 units
-constexpr float CODE_SCALE = 16777216.f; // 2^24: undoes the subnormal encoding
+constexpr float CODE_SHIFT = 16384.f;    // 2^14: code * 2^-24 (subnormal) -> code * 2^-10
+constexpr float CODE_UNIT = 1024.f;      // 2^10: undoes the codes' scale in the MFMAs
+constexpr float SUB_UNIT = 16777216.f;   // 2^24: undoes the subnormal encoding of K codes
 constexpr float LO_SCALE = 2048.f;       // 2^11: lo half of a packed softmax weight
 constexpr float LO_INV = 1.f / 2048.f;
 constexpr float INT4_HI = 16.f;          // high nibbles enter the MFMAs as code * 16
+// V codes enter the PV MFMA centred on their mid-range, code - mid, and a
+// token's zero point becomes zero + mid * scale: the products and the zero
+// sum then stay near the output's own magnitude instead of cancelling (int8
+// codes 0..255 times scale reach |zero|, and sum p*code*scale and sum
+// p*zero nearly cancel in the mean of zero-mean data).
+template <int FMT> constexpr float vmid() { return FMT == FMT_INT8 ? 128.f : 8.f; }
 constexpr int RSRC_WORD3 = 0x00020000;   // gfx9 raw buffer: 32-bit data format
 constexpr int CPOL_NT = 2;               // nontemporal: every byte is used once
 // Cache policy of the K/V payload loads. Head-major rows stream as
@@ -257,6 +269,18 @@ template <int FMT, int D, int GQ, int G> struct TileBuf {
   Raw<Gm::QMETA ? 4 * Gm::PASSES : 4> kmr[2], vmr[2];
 };
 
+// Two V codes as byte- or nibble-built binary16 subnormals (code * 2^-24) to
+// (code - mid) * 2^-10: one packed binary16 fma, exact (the results are
+// integers below 2^8 in magnitude times 2^-10, so normal or zero). Measured
+// on gfx950 against the double-precision reference: centred subnormal codes
+// left int4:32 at 64k tokens at rel_l2 1.0e-4 and int8:64 with outlier
+// channels at 32k at 9e-6; normal-range codes 3.1e-6 and 1.2e-6.
+__device__ __forceinline__ uint32_t centre_codes(uint32_t w, float mid) {
+  const _Float16 m = (_Float16)(mid * (1.f / CODE_UNIT));
+  const half2_t h = as_h2(w) * (half2_t){(_Float16)CODE_SHIFT, (_Float16)CODE_SHIFT} - (half2_t){m, m};
+  return __builtin_bit_cast(uint32_t, h);
+}
+
 // Broadcast of quad lane I's value to the whole quad (DPP quad_perm).
 template <int I> __device__ __forceinline__ uint32_t quad_bcast(uint32_t x) {
   return (uint32_t)__builtin_amdgcn_mov_dpp((int)x, I * 0x55, 0xF, 0xF, false);
@@ -315,7 +339,7 @@ __device__ __forceinline__ void decode_item(const Args &a, const Ext &x, const i
   constexpr int DEPTH = depth_of<U>();
   constexpr bool HL_LDS = HL && hl_lds_fits<D, G>(WPB);
   constexpr int NQ = HL ? 1 : 2;                   // query operands per k-step
-  constexpr float UNIT = QUANT ? CODE_SCALE : 1.f; // log2 units per score unit
+  constexpr float UNIT = QUANT ? SUB_UNIT : 1.f; // log2 units per score unit
   constexpr float TAU_S = TAU / UNIT;
   using Buf = TileBuf<FMT, D, GQ, G>;
 
@@ -730,12 +754,12 @@ __device__ __forceinline__ void decode_item(const Args &a, const Ext &x, const i
         float w = pj[i];
         if constexpr (QUANT) {
           const uint32_t mv = vmeta[p][i];
-          zacc[p] = fmaf(pj[i], hi_f(mv), zacc[p]);
+          zacc[p] = fmaf(pj[i], fmaf(vmid<FMT>(), lo_f(mv), hi_f(mv)), zacc[p]);
           w *= lo_f(mv);
         }
         w = col_live ? w : 0.f;
-        const _Float16 hi = (_Float16)w;
         if constexpr (HL) {
+          const _Float16 hi = (_Float16)w;
           // the lo half has its own accumulator rows, so it enters scaled by
           // 2^11 (it never exceeds the hi half, so this cannot overflow) and
           // stays out of the binary16 subnormal range; the rows are scaled
@@ -743,6 +767,7 @@ __device__ __forceinline__ void decode_item(const Args &a, const Ext &x, const i
           const _Float16 lo = (_Float16)((w - (float)hi) * LO_SCALE);
           pa[p][0][i] = col_lo ? lo : hi;
         } else {
+          const _Float16 hi = (_Float16)w;
           const _Float16 lo = (_Float16)(w - (float)hi);
           pa[p][0][i] = hi;
           pa[p][NQ - 1][i] = lo;
@@ -760,14 +785,14 @@ __device__ __forceinline__ void decode_item(const Args &a, const Ext &x, const i
         if constexpr (FMT == FMT_F16) {
           bw[q2] = perm(tb.w[e / 2], ta.w[e / 2], (e & 1) ? 0x07060302u : 0x05040100u);
         } else if constexpr (FMT == FMT_INT8) {
-          bw[q2] = perm(tb.w[e / 4], ta.w[e / 4], sel_pair(e & 3));
+          bw[q2] = centre_codes(perm(tb.w[e / 4], ta.w[e / 4], sel_pair(e & 3)), 128.f);
         } else {
           // odd dims (high nibbles) stay in place: code * 16, undone with
           // the code scale at the wave's result
           const uint32_t msk = (e & 1) ? 0xF0F0F0F0u : 0x0F0F0F0Fu;
           const uint32_t na = ta.w[0] & msk;
           const uint32_t nb = tb.w[0] & msk;
-          bw[q2] = perm(nb, na, sel_pair((e >> 1) & 3));
+          bw[q2] = centre_codes(perm(nb, na, sel_pair((e >> 1) & 3)), (e & 1) ? 8.f * INT4_HI : 8.f);
         }
       }
       const half8_t bv = __builtin_bit_cast(half8_t, (u32x4_t){bw[0], bw[1], bw[2], bw[3]});
@@ -864,7 +889,7 @@ __device__ __forceinline__ void decode_item(const Args &a, const Ext &x, const i
         float *dst = (lo_half ? sL : sO) + (wave * G + pr % G) * D + c * EV;
 #pragma unroll
         for (int e = 0; e < EV; ++e)
-          dst[e] = QUANT ? fmaf(acc[p][e][i], (lo_half ? CODE_SCALE * LO_INV : CODE_SCALE) * vdim_scale<FMT>(e),
+          dst[e] = QUANT ? fmaf(acc[p][e][i], (lo_half ? CODE_UNIT * LO_INV : CODE_UNIT) * vdim_scale<FMT>(e),
                                 lo_half ? 0.f : zrow[p][i])
                          : acc[p][e][i] * (lo_half ? LO_INV : 1.f);
       }
@@ -1287,8 +1312,10 @@ hipError_t launch_group(const Args &a, const Ext &x, const Launch &l, hipStream_
     // crowd out the long ones; a batch of 16 sequences with log-uniform
     // lengths up to 128k took 145 us fused on it against 94 us on the
     // (splits, heads, B) grid)
+    // (a 1-D grid holds at most 2^32 - 1 work-items: larger steps keep the
+    // 3-D grid)
     if (ORD == ORD_HEAD && !x.seq_lens && di.nx > 1 && nhg % di.nx == 0 &&
-        (long long)a.splits * nhg <= 0x7fffffff) {
+        (long long)a.splits * nhg * block.x <= 0xffffffffLL) {
       xk.nx = di.nx;
       grid = dim3((unsigned)(a.splits * nhg));
     }

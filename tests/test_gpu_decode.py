@@ -22,6 +22,12 @@ pytestmark = pytest.mark.gpu
 
 REL_TOL = 2e-3
 ABS_TOL_F16 = 2e-3
+# Tight bounds on the benchmarked plans, beside the reference's 2e-3 bar: the
+# reference's own kernels reach 2.4e-6 (int8) and 2.4e-6 (int4) over its
+# sweep (results/sweep_rtx5060-laptop.csv, err_ref); these plans measure
+# 1.2e-6 (int8:64 with outlier channels, 32k), 3.1e-6 (int4:32, 64k) and
+# ~3e-7 (f16), so a tenfold loss of precision fails here.
+TIGHT = {R.FMT_INT8: 1e-5, R.FMT_INT4: 2e-5, R.FMT_F16: 5e-6}
 
 
 @pytest.fixture(scope="module", autouse=True)
@@ -165,7 +171,8 @@ def test_north_star_int8_32k():
         for unroll, warps in ((2, 4), (4, 8)):
             check(b, run(b, splits, unroll=unroll, warps=warps), f"S={splits} u{unroll} w{warps}")
     # the plan bench.py times for the headline metric: 32 splits, 4 waves, u2
-    check(b, run(b, 32, unroll=2, warps=4), "benchmarked plan S=32 u2 w4")
+    err = check(b, run(b, 32, unroll=2, warps=4), "benchmarked plan S=32 u2 w4")
+    assert err < TIGHT[R.FMT_INT8], err
     # accuracy against the exact fp32 attention stays near the calibrated budget
     # against exact fp32 attention the error is the quantizer's, as the
     # oracle's own dequantised reference shows
@@ -180,6 +187,8 @@ def test_north_star_f16_32k():
     b = build(Case(1, 32, 8, 128, 32768, R.FMT_F16, 0, R.ORD_HEAD, 0, seed=1))
     for splits in (1, 64):
         check(b, run(b, splits), f"S={splits}")
+    err = check(b, run(b, 32, unroll=2, warps=4), "S=32 u2 w4")
+    assert err < TIGHT[R.FMT_F16], err
 
 
 def test_long_context_int4_64k():
@@ -188,7 +197,8 @@ def test_long_context_int4_64k():
     for splits in (8, 256):
         check(b, run(b, splits), f"S={splits}")
     # the plan bench.py --config 4 times: 32 splits, 8 waves, u2
-    check(b, run(b, 32, unroll=2, warps=8), "benchmarked plan S=32 u2 w8")
+    err = check(b, run(b, 32, unroll=2, warps=8), "benchmarked plan S=32 u2 w8")
+    assert err < TIGHT[R.FMT_INT4], err
 
 
 @pytest.mark.parametrize("order", [R.ORD_HEAD, R.ORD_TOKEN])
@@ -408,8 +418,9 @@ def test_fused_merge_matches_two_launch(fmt, group, order, bt, G):
     Hkv = H // 4 if G == 1 else H // G
     b = build(Case(2, H, Hkv, 128, 1500, fmt, group, order, bt, seed=11))
     counters = R.fused_counters(2, Hkv if G > 1 else H)
-    # (past 32 splits the last workgroup keeps two chunks of loads in flight:
-    # an even and an odd chunk count, several rounds)
+    # (past 32 splits the last workgroup folds the splits in chunks of 32, one
+    # memory round trip per chunk: an even and an odd chunk count, several
+    # chunks, and a chunk that ends past the split count)
     for splits, warps, unroll in ((8, 4, 2), (13, 8, 4), (64, 4, 4), (97, 4, 2), (200, 4, 2)):
         two = run(b, splits, pack=G > 1, unroll=unroll, warps=warps)
         b.out.fill_(float("nan"))
