@@ -16,6 +16,7 @@
 #ifndef KVF_ABI_H
 #define KVF_ABI_H
 
+#include <stddef.h>
 #include <stdint.h>
 #include <hip/hip_runtime_api.h>
 
@@ -85,6 +86,14 @@ typedef struct kvf_varlen_args {
 } kvf_varlen_args_t;
 #endif
 
+/* Version of this C ABI, also returned by kvf_abi_version(). 2: the one-launch
+ * (kvf_launch_fused_variant), persistent and timed-step entry points take
+ * the sizes of their counter and queue buffers, in 32-bit words, and reject
+ * buffers that are too small; VarlenArgs carries `flags`. Version 1 took the
+ * buffers without sizes, and its VarlenArgs had three fields (24 bytes).
+ * A caller built against another version checks kvf_abi_version() at load. */
+#define KVF_ABI_VERSION 2
+
 /* VarlenArgs::flags. LONGEST_FIRST (batches of 2..64 sequences): workgroups
  * take sequences in decreasing length, so the longest sequences' workgroups
  * are dispatched first and the short ones fill the tail. The output is
@@ -119,20 +128,26 @@ hipError_t kvf_launch_varlen_variant(const char *variant_id, const kvf_args_t *a
 
 /* Unsigned ints per merge counter of the one-launch step: each counter has a
  * 128-byte line of its own, so the arrivals of different head groups do not
- * serialise on one line. */
+ * serialise on one line. A step of B sequences needs
+ * KVF_COUNTER_WORDS(B, head groups) of them, head groups = Hkv for GQA-packed
+ * variants ("_g2_" and up) and H otherwise. */
 #define KVF_COUNTER_STRIDE 32
+#define KVF_COUNTER_WORDS(B, head_groups) ((size_t)(B) * (size_t)(head_groups) * KVF_COUNTER_STRIDE)
+/* Unsigned ints of the persistent step's work queue. */
+#define KVF_QUEUE_WORDS (2 * KVF_COUNTER_STRIDE)
 
 /* One decode step in a single kernel launch: the last workgroup of each
  * (sequence, head group) merges the splits, which removes the reference's
  * second (merge) launch (runtime/kvf_kernels.cuh:315-318). `counters` is
- * caller-owned device memory of B * (pack > 1 ? Hkv : H) * KVF_COUNTER_STRIDE
- * unsigned ints, zero before the first call; every call leaves it zero again. Calls that run
- * concurrently (on different streams) need distinct counters, exactly as
- * they need distinct part_o / part_ml. `va` may be NULL. Outputs match
- * kvf_launch_variant to rounding. */
+ * caller-owned device memory of `counter_words` unsigned ints, at least
+ * KVF_COUNTER_WORDS(B, pack > 1 ? Hkv : H) (hipErrorInvalidValue otherwise,
+ * before anything is launched), zero before the first call; every call
+ * leaves it zero again. Calls that run concurrently (on different streams)
+ * need distinct counters, exactly as they need distinct part_o / part_ml.
+ * `va` may be NULL. Outputs match kvf_launch_variant to rounding. */
 hipError_t kvf_launch_fused_variant(const char *variant_id, const kvf_args_t *a,
                                     const kvf_varlen_args_t *va, unsigned *counters,
-                                    hipStream_t stream);
+                                    size_t counter_words, hipStream_t stream);
 
 /* The persistent step: one launch whose workgroups, at most as many as are
  * resident at once (`workgroups` > 0 caps them further), work through a
@@ -144,16 +159,19 @@ hipError_t kvf_launch_fused_variant(const char *variant_id, const kvf_args_t *a,
  * group by head group, split by split. With `counters` (as in
  * kvf_launch_fused_variant) the last workgroup of each head group merges its
  * splits inside the launch; with counters == NULL the merge kernel follows,
- * as in kvf_launch_varlen_variant. `queue` is caller-owned device memory of
- * 2 * KVF_COUNTER_STRIDE unsigned ints, zero before the first call; every
- * call leaves it zero again, and concurrent calls need distinct queues.
+ * as in kvf_launch_varlen_variant. `counter_words` is the size of `counters` (0
+ * with no counters), checked as for kvf_launch_fused_variant. `queue` is
+ * caller-owned device memory of `queue_words` >= KVF_QUEUE_WORDS unsigned
+ * ints, zero before the first call; every call leaves it zero again, and
+ * concurrent calls need distinct queues.
  * `va` may be NULL. Outputs equal kvf_launch_fused_variant's (counters) or
  * kvf_launch_varlen_variant's (no counters) bit for bit. Unroll-2 variants
  * only ("_u2_" ids); others return hipErrorInvalidValue. No counterpart in
  * the reference, which launches one block per (split, head). */
 hipError_t kvf_launch_persistent_variant(const char *variant_id, const kvf_args_t *a,
                                          const kvf_varlen_args_t *va, unsigned *counters,
-                                         unsigned *queue, int workgroups, hipStream_t stream);
+                                         size_t counter_words, unsigned *queue,
+                                         size_t queue_words, int workgroups, hipStream_t stream);
 
 /* Bytes of the device scratch array behind kvf_launch_fused_variant_noalloc. */
 #define KVF_SCRATCH_BYTES (16u << 20)
@@ -164,10 +182,14 @@ hipError_t kvf_launch_persistent_variant(const char *variant_id, const kvf_args_
  * process ends, so Args::part_o and Args::part_ml are ignored. No counterpart
  * in the reference; it is for callers that cannot allocate (code under HIP
  * graph capture, tight serving loops). Returns hipErrorInvalidValue when the
- * step's counters (B * (pack > 1 ? Hkv : H) * KVF_COUNTER_STRIDE unsigned ints,
- * at most 64 KiB) or
- * partials (B*H*splits*(d+2) floats) do not fit. Calls that overlap on one GPU
- * share the array and race; run them on one stream. */
+ * step's counters (KVF_COUNTER_WORDS(B, pack > 1 ? Hkv : H) unsigned ints, at
+ * most 64 KiB) or partials (B*H*splits*(d+2) floats) do not fit. The first
+ * call on a device (and the first of each variant) sets up: it looks up the
+ * array's device address and the device's CU and XCD counts and queries the
+ * kernel's occupancy, none of which allocates; make one call per variant
+ * before capturing a graph, after which a call only enqueues the kernel (no
+ * memset: the kernel returns its counters to zero itself). Calls that overlap
+ * on one GPU share the array and race; run them on one stream. */
 hipError_t kvf_launch_fused_variant_noalloc(const char *variant_id, const kvf_args_t *a,
                                             const kvf_varlen_args_t *va,
                                             hipStream_t stream);
@@ -195,14 +217,16 @@ hipError_t kvf_launch_partial_varlen_variant_timed(const char *variant_id, const
                                                    hipEvent_t stop);
 
 /* One whole decode step, as kvf_launch_varlen_variant (`va` may be NULL) or,
- * when `counters` is not NULL, as kvf_launch_fused_variant, with `start` and
+ * when `counters` is not NULL, as kvf_launch_fused_variant (`counter_words`
+ * its size, checked the same way), with `start` and
  * `stop` (created by the caller with timing enabled) bound to the split
  * kernel's own dispatch: hipEventElapsedTime(start, stop) is that kernel's
  * execution time inside the step, the merge launch (if any) following it as
  * it does in every step. Harness use, no counterpart in the reference. */
 hipError_t kvf_launch_step_timed(const char *variant_id, const kvf_args_t *a,
                                  const kvf_varlen_args_t *va, unsigned *counters,
-                                 hipStream_t stream, hipEvent_t start, hipEvent_t stop);
+                                 size_t counter_words, hipStream_t stream, hipEvent_t start,
+                                 hipEvent_t stop);
 
 /* Only the log-sum-exp merge (runtime/kvf_kernels.cuh:288-306) of the
  * partials named by `a` (B, H, splits, part_o, part_ml, out) for head
@@ -244,6 +268,9 @@ hipError_t kvf_append_tokens(int fmt, int group, int d, const float *x,
 
 /* Library version string. */
 const char *kvf_version(void);
+
+/* KVF_ABI_VERSION of the library's build. */
+int kvf_abi_version(void);
 
 #ifdef __cplusplus
 } /* extern "C" */

@@ -32,6 +32,20 @@ Registry &registry() {
 
 LaunchXFn extended(const char *id) { return id ? registry().findx(id) : nullptr; }
 
+// GQA pack size of a variant id ("_g{G}_"), 1 when absent.
+int pack_of(const char *id) {
+  const char *g = std::strstr(id, "_g");
+  return g ? std::max(1, std::atoi(g + 2)) : 1;
+}
+
+// Whether `words` unsigned ints hold the fused step's merge counters for `a`
+// (one KVF_COUNTER_STRIDE line per (sequence, head group)).
+bool counters_fit(const char *id, const kvf_args_t &a, size_t words) {
+  if (a.B < 1 || a.H < 1 || a.Hkv < 1) return false;
+  const size_t groups = pack_of(id) > 1 ? (size_t)a.Hkv : (size_t)a.H;
+  return words >= KVF_COUNTER_WORDS(a.B, groups);
+}
+
 Ext ext_of(const kvf_varlen_args_t *va) {
   Ext x;
   if (va) {
@@ -167,10 +181,11 @@ extern "C" hipError_t kvf_launch_varlen_variant(const char *id, const kvf_args_t
 
 extern "C" hipError_t kvf_launch_fused_variant(const char *id, const kvf_args_t *a,
                                                const kvf_varlen_args_t *va, unsigned *counters,
-                                               hipStream_t st) {
+                                               size_t counter_words, hipStream_t st) {
   if (!a || !counters) return hipErrorInvalidValue;
   const LaunchXFn fx = extended(id);
   if (!fx) return hipErrorNotFound;
+  if (!counters_fit(id, *a, counter_words)) return hipErrorInvalidValue;
   Ext x = ext_of(va);
   x.counters = counters;
   return fx(*a, x, Launch{}, st);
@@ -178,10 +193,13 @@ extern "C" hipError_t kvf_launch_fused_variant(const char *id, const kvf_args_t 
 
 extern "C" hipError_t kvf_launch_persistent_variant(const char *id, const kvf_args_t *a,
                                                     const kvf_varlen_args_t *va, unsigned *counters,
-                                                    unsigned *queue, int workgroups, hipStream_t st) {
+                                                    size_t counter_words, unsigned *queue,
+                                                    size_t queue_words, int workgroups, hipStream_t st) {
   if (!a || !queue || workgroups < 0) return hipErrorInvalidValue;
   const LaunchXFn fx = extended(id);
   if (!fx) return hipErrorNotFound;
+  if (queue_words < KVF_QUEUE_WORDS) return hipErrorInvalidValue;
+  if (counters && !counters_fit(id, *a, counter_words)) return hipErrorInvalidValue;
   Ext x = ext_of(va);
   x.counters = counters;
   x.queue = queue;
@@ -235,9 +253,7 @@ extern "C" hipError_t kvf_launch_fused_variant_noalloc(const char *id, const kvf
   const LaunchXFn fx = extended(id);
   if (!fx) return hipErrorNotFound;
   // counters: one per (sequence, head group); the pack size comes from the id
-  const char *g = std::strstr(id, "_g");
-  const int pack = g ? std::atoi(g + 2) : 1;
-  const size_t counters = (size_t)a->B * (pack > 1 ? a->Hkv : a->H) * KVF_COUNTER_STRIDE * sizeof(unsigned);
+  const size_t counters = KVF_COUNTER_WORDS(a->B, pack_of(id) > 1 ? a->Hkv : a->H) * sizeof(unsigned);
   const size_t heads = (size_t)a->B * a->H * a->splits;
   const size_t d = std::strstr(id, "_d64") ? 64 : 128;
   const size_t ml_bytes = align256(heads * 2 * sizeof(float));
@@ -297,10 +313,12 @@ extern "C" hipError_t kvf_launch_partial_varlen_variant_timed(const char *id, co
 
 extern "C" hipError_t kvf_launch_step_timed(const char *id, const kvf_args_t *a,
                                             const kvf_varlen_args_t *va, unsigned *counters,
-                                            hipStream_t st, hipEvent_t start, hipEvent_t stop) {
+                                            size_t counter_words, hipStream_t st, hipEvent_t start,
+                                            hipEvent_t stop) {
   if (!a || !start || !stop) return hipErrorInvalidValue;
   const LaunchXFn fx = extended(id);
   if (!fx) return hipErrorNotFound;
+  if (counters && !counters_fit(id, *a, counter_words)) return hipErrorInvalidValue;
   Ext x = ext_of(va);
   x.counters = counters;
   Launch l;
@@ -378,4 +396,6 @@ extern "C" hipError_t kvf_append_tokens(int fmt, int group, int d, const float *
                        max_blocks, data, meta, st);
 }
 
-extern "C" const char *kvf_version(void) { return "kvforge-mi355x 0.1 (gfx950)"; }
+extern "C" const char *kvf_version(void) { return "kvforge-mi355x 0.3 (gfx950, ABI 2)"; }
+
+extern "C" int kvf_abi_version(void) { return KVF_ABI_VERSION; }

@@ -18,6 +18,8 @@ ORD_HEAD, ORD_TOKEN = 0, 1
 FMT_NAMES = {FMT_F16: "f16", FMT_INT8: "int8", FMT_INT4: "int4"}
 FMT_BY_NAME = {v: k for k, v in FMT_NAMES.items()}
 
+ABI_VERSION = 2  # KVF_ABI_VERSION of include/kvf_abi.h
+
 HIP_SUCCESS = 0
 HIP_ERROR_INVALID_VALUE = 1
 HIP_ERROR_NOT_FOUND = 500
@@ -71,11 +73,12 @@ def hip_lib():
     L.kvf_launch_varlen_variant.argtypes = [ctypes.c_char_p, ctypes.POINTER(Args),
                                             ctypes.POINTER(VarlenArgs), P]
     L.kvf_launch_fused_variant.restype = I
+    Z = ctypes.c_size_t
     L.kvf_launch_fused_variant.argtypes = [ctypes.c_char_p, ctypes.POINTER(Args),
-                                           ctypes.POINTER(VarlenArgs), P, P]
+                                           ctypes.POINTER(VarlenArgs), P, Z, P]
     L.kvf_launch_persistent_variant.restype = I
     L.kvf_launch_persistent_variant.argtypes = [ctypes.c_char_p, ctypes.POINTER(Args),
-                                                ctypes.POINTER(VarlenArgs), P, P, I, P]
+                                                ctypes.POINTER(VarlenArgs), P, Z, P, Z, I, P]
     L.kvf_launch_fused_variant_noalloc.restype = I
     L.kvf_launch_fused_variant_noalloc.argtypes = [ctypes.c_char_p, ctypes.POINTER(Args),
                                                    ctypes.POINTER(VarlenArgs), P]
@@ -88,7 +91,7 @@ def hip_lib():
                                                          ctypes.POINTER(VarlenArgs), P, P, P]
     L.kvf_launch_step_timed.restype = I
     L.kvf_launch_step_timed.argtypes = [ctypes.c_char_p, ctypes.POINTER(Args),
-                                        ctypes.POINTER(VarlenArgs), P, P, P, P]
+                                        ctypes.POINTER(VarlenArgs), P, Z, P, P, P]
     L.kvf_launch_merge.restype = I
     L.kvf_launch_merge.argtypes = [I, ctypes.POINTER(Args), P]
     L.kvf_variant_count.restype = I
@@ -101,6 +104,11 @@ def hip_lib():
     L.kvf_append_tokens.argtypes = [I, I, I, P, I, I, I, P, I, I, P, I, P, P, P]
     L.kvf_version.restype = ctypes.c_char_p
     L.kvf_version.argtypes = []
+    L.kvf_abi_version.restype = I
+    L.kvf_abi_version.argtypes = []
+    if L.kvf_abi_version() != ABI_VERSION:
+        raise KvfError(f"{HIP_LIB} has C ABI version {L.kvf_abi_version()}, this binding "
+                       f"expects {ABI_VERSION}: rebuild the library")
     _hip = L
     return L
 
@@ -142,6 +150,11 @@ def variants():
 
 def _ptr(t):
     return None if t is None else ctypes.c_void_p(t.data_ptr())
+
+
+def _words(t):
+    """Size in 32-bit words of a counter or queue buffer (0 for None)."""
+    return 0 if t is None else t.numel() * t.element_size() // 4
 
 
 def make_args(q, k, v, k_meta, v_meta, table, out, part_o, part_ml, B, H, Hkv, n,
@@ -187,6 +200,7 @@ def launch_partial(vid, args, stream=None):
 
 
 COUNTER_STRIDE = 32  # KVF_COUNTER_STRIDE: unsigned ints per merge counter
+QUEUE_WORDS = 2 * COUNTER_STRIDE  # KVF_QUEUE_WORDS
 
 
 def fused_counters(B, head_groups, device="cuda:0"):
@@ -212,7 +226,8 @@ def launch_fused(vid, args, counters, varlen=None, stream=None, flags=0):
     if varlen is not None:
         va = ctypes.byref(_varlen_args(*varlen, flags=flags))
     err = hip_lib().kvf_launch_fused_variant(vid.encode(), ctypes.byref(args), va,
-                                             _ptr(counters), stream_handle(stream))
+                                             _ptr(counters), _words(counters),
+                                             stream_handle(stream))
     check(err, f"kvf_launch_fused_variant({vid})")
 
 
@@ -220,7 +235,7 @@ def persistent_queue(device="cuda:0"):
     """Zeroed work queue for kvf_launch_persistent_variant (claim counter and
     done counter, one 128-byte line each), left zero by every call."""
     import torch
-    return torch.zeros(2 * COUNTER_STRIDE, dtype=torch.int32, device=device)
+    return torch.zeros(QUEUE_WORDS, dtype=torch.int32, device=device)
 
 
 def launch_persistent(vid, args, queue, counters=None, varlen=None, workgroups=0, stream=None, flags=0):
@@ -232,8 +247,9 @@ def launch_persistent(vid, args, queue, counters=None, varlen=None, workgroups=0
     if varlen is not None:
         va = ctypes.byref(_varlen_args(*varlen, flags=flags))
     err = hip_lib().kvf_launch_persistent_variant(vid.encode(), ctypes.byref(args), va,
-                                                  _ptr(counters) if counters is not None else None,
-                                                  _ptr(queue), workgroups, stream_handle(stream))
+                                                  _ptr(counters), _words(counters),
+                                                  _ptr(queue), _words(queue), workgroups,
+                                                  stream_handle(stream))
     check(err, f"kvf_launch_persistent_variant({vid})")
 
 

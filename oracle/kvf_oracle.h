@@ -86,27 +86,27 @@ void kvfo_reference_attention(int B, int H, int Hkv, int D, int n,
                               const float *q, const float *K, const float *V,
                               float scale, float *out);
 
-/* Variable-length extension (this build's definition): sequence b uses the
- * first lens[b] tokens of its rows; K/V are [B][Hkv][n_max][D]. */
 /* As kvfo_reference_attention, over `threads` host threads (same output). */
 void kvfo_reference_attention_mt(int B, int H, int Hkv, int D, int n,
                                  const float *q, const float *K, const float *V,
                                  float scale, float *out, int threads);
-/* As kvfo_reference_attention_varlen, over `threads` host threads. */
-// The varlen reference over ragged arrays (kvfo_make_data_ragged's layout):
-// sequence b's rows start at Hkv * (lens[0] + ... + lens[b-1]), head by head.
-// Pinned against kvfo_reference_attention_varlen on the padded arrays.
-void kvfo_reference_attention_ragged_mt(int B, int H, int Hkv, int D, const int32_t *lens,
-                                        const float *q, const float *K, const float *V,
-                                        float scale, float *out, int threads);
-void kvfo_reference_attention_varlen_mt(int B, int H, int Hkv, int D, int n_max,
-                                        const int32_t *lens, const float *q,
-                                        const float *K, const float *V, float scale,
-                                        float *out, int threads);
+/* Variable-length extension (this build's definition): sequence b uses the
+ * first lens[b] tokens of its rows; K/V are [B][Hkv][n_max][D]. */
 void kvfo_reference_attention_varlen(int B, int H, int Hkv, int D, int n_max,
                                      const int32_t *lens, const float *q,
                                      const float *K, const float *V,
                                      float scale, float *out);
+/* As kvfo_reference_attention_varlen, over `threads` host threads. */
+void kvfo_reference_attention_varlen_mt(int B, int H, int Hkv, int D, int n_max,
+                                        const int32_t *lens, const float *q,
+                                        const float *K, const float *V, float scale,
+                                        float *out, int threads);
+/* The varlen reference over ragged arrays (kvfo_make_data_ragged's layout):
+ * sequence b's rows start at Hkv * (lens[0] + ... + lens[b-1]), head by head.
+ * Pinned against kvfo_reference_attention_varlen on the padded arrays. */
+void kvfo_reference_attention_ragged_mt(int B, int H, int Hkv, int D, const int32_t *lens,
+                                        const float *q, const float *K, const float *V,
+                                        float scale, float *out, int threads);
 
 double kvfo_rel_l2(const float *a, const float *ref, long long n);
 float kvfo_scale_log2(int D);

@@ -102,6 +102,39 @@ def test_planned_program_library_exports_its_entry_points():
 
 
 @pytest.mark.skipif(not os.path.exists(R.HIP_LIB), reason="libkvf_hip.so not built")
+def test_sized_buffers_are_checked_before_any_device_call():
+    # ABI version 2: the fused, persistent and timed-step entry points take
+    # the sizes of their counter and queue buffers and reject buffers that
+    # are too small, before touching the device (a caller sized to the
+    # version-1 contract, one word per head group, gets hipErrorInvalidValue
+    # instead of out-of-bounds atomics)
+    lib = R.hip_lib()
+    assert lib.kvf_abi_version() == R.ABI_VERSION == 2
+    text = open(os.path.join(INCLUDE, "kvf_abi.h")).read()
+    assert "#define KVF_ABI_VERSION 2" in text
+    assert "#define KVF_QUEUE_WORDS (2 * KVF_COUNTER_STRIDE)" in text
+    assert "ABI 2" in lib.kvf_version().decode()
+    a = R.Args()
+    a.B, a.H, a.Hkv, a.n, a.splits, a.warps, a.group_shift = 2, 32, 8, 4096, 32, 4, 6
+    buf = ctypes.create_string_buffer(4 * 4096)  # host memory: never dereferenced
+    p = ctypes.cast(buf, ctypes.c_void_p)
+    need = 2 * 8 * R.COUNTER_STRIDE  # B x head groups (pack 4: Hkv) x stride
+    for vid, groups in ((b"int8_hm_c_g4_u2_d128", 8), (b"int8_hm_c_g1_u2_d128", 32)):
+        need = 2 * groups * R.COUNTER_STRIDE
+        for words in (0, 2 * groups, need - 1):
+            assert lib.kvf_launch_fused_variant(vid, ctypes.byref(a), None, p, words,
+                                                None) == R.HIP_ERROR_INVALID_VALUE, (vid, words)
+            assert lib.kvf_launch_step_timed(vid, ctypes.byref(a), None, p, words, None, p,
+                                             p) == R.HIP_ERROR_INVALID_VALUE, (vid, words)
+            assert lib.kvf_launch_persistent_variant(vid, ctypes.byref(a), None, p, words, p,
+                                                     R.QUEUE_WORDS, 0,
+                                                     None) == R.HIP_ERROR_INVALID_VALUE, (vid, words)
+    # no counters at all is not a fused step either
+    assert lib.kvf_launch_fused_variant(b"int8_hm_c_g4_u2_d128", ctypes.byref(a), None, None, 0,
+                                        None) == R.HIP_ERROR_INVALID_VALUE
+
+
+@pytest.mark.skipif(not os.path.exists(R.HIP_LIB), reason="libkvf_hip.so not built")
 def test_noalloc_entry_rejects_steps_beyond_its_scratch():
     # kvf_launch_fused_variant_noalloc checks the step's counters and partials
     # against its fixed device scratch (KVF_SCRATCH_BYTES) before touching the

@@ -119,12 +119,16 @@ def test_persistent_rejects_bad_arguments():
     queue = R.persistent_queue()
     qp = ctypes.c_void_p(queue.data_ptr())
     vid_ = b"int8_hm_c_g4_u2_d128"
-    assert L.kvf_launch_persistent_variant(vid_, ctypes.byref(a), None, None, None, 0, None) == \
+    qw = R.QUEUE_WORDS
+    assert L.kvf_launch_persistent_variant(vid_, ctypes.byref(a), None, None, 0, None, 0, 0, None) == \
         R.HIP_ERROR_INVALID_VALUE
-    assert L.kvf_launch_persistent_variant(vid_, ctypes.byref(a), None, None, qp, -1, None) == \
+    assert L.kvf_launch_persistent_variant(vid_, ctypes.byref(a), None, None, 0, qp, qw, -1, None) == \
         R.HIP_ERROR_INVALID_VALUE
-    assert L.kvf_launch_persistent_variant(b"int8_hm_c_g4_u2_d96", ctypes.byref(a), None, None, qp, 0,
-                                           None) == R.HIP_ERROR_NOT_FOUND
+    # a queue shorter than KVF_QUEUE_WORDS
+    assert L.kvf_launch_persistent_variant(vid_, ctypes.byref(a), None, None, 0, qp, qw - 1, 0, None) == \
+        R.HIP_ERROR_INVALID_VALUE
+    assert L.kvf_launch_persistent_variant(b"int8_hm_c_g4_u2_d96", ctypes.byref(a), None, None, 0, qp, qw,
+                                           0, None) == R.HIP_ERROR_NOT_FOUND
     # the persistent kernels are built for unroll 2
-    assert L.kvf_launch_persistent_variant(b"int8_hm_c_g4_u4_d128", ctypes.byref(a), None, None, qp, 1,
-                                           None) == R.HIP_ERROR_INVALID_VALUE
+    assert L.kvf_launch_persistent_variant(b"int8_hm_c_g4_u4_d128", ctypes.byref(a), None, None, 0, qp, qw,
+                                           1, None) == R.HIP_ERROR_INVALID_VALUE

@@ -97,3 +97,53 @@ def test_noalloc_varlen_f16():
     err = O.rel_l2(got, ref)
     print(f"  varlen f16 q/out S=8: rel_l2={err:.3g}", flush=True)
     assert np.all(np.isfinite(got)) and err < 2e-3
+
+
+def test_noalloc_allocates_nothing_and_replays_in_a_graph():
+    # after one call (the per-device and per-variant set-up), further calls
+    # leave the device's free memory unchanged, and the step captured into a
+    # HIP graph (one kernel node: the kernel returns its counters to zero
+    # itself, so no memset is recorded) replays with the eager result, on two
+    # different queries and back, with eager work between the replays
+    b = build(Case(1, 32, 8, 128, 4096, R.FMT_INT8, 64, R.ORD_HEAD, 0, seed=34))
+    v = vid(b, True, 2)
+    a = args(b, 1, 4)
+    a.splits = 32
+    a.part_o = None
+    a.part_ml = None
+    assert _noalloc(v, a) == R.HIP_SUCCESS
+    torch.cuda.synchronize()
+    free0 = torch.cuda.mem_get_info()[0]
+    for _ in range(3):
+        assert _noalloc(v, a) == R.HIP_SUCCESS
+    torch.cuda.synchronize()
+    assert torch.cuda.mem_get_info()[0] == free0
+    q0 = b.q.clone()
+    eager = []
+    for scale in (1.0, -0.5):
+        b.q.copy_(q0 * scale)
+        b.out.fill_(float("nan"))
+        assert _noalloc(v, a) == R.HIP_SUCCESS
+        torch.cuda.synchronize()
+        eager.append(b.out.clone())
+    b.q.copy_(q0)
+    g = torch.cuda.CUDAGraph()
+    s = torch.cuda.Stream()
+    with torch.cuda.graph(g, stream=s):
+        assert _noalloc(v, a) == R.HIP_SUCCESS
+    torch.cuda.synchronize()
+    for r, scale in enumerate((1.0, -0.5, 1.0, -0.5)):
+        b.q.copy_(q0 * scale)
+        b.out.fill_(float("nan"))
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        want = eager[0 if scale == 1.0 else 1]
+        assert torch.equal(b.out, want), f"replay {r}"
+    b.q.copy_(q0)
+    b.out.fill_(float("nan"))
+    g.replay()
+    torch.cuda.synchronize()
+    err = O.rel_l2(b.out.cpu().numpy(), reference(b))
+    print(f"  graph replay of the no-alloc step: rel_l2={err:.3g}", flush=True)
+    assert err < 2e-3
