@@ -4,11 +4,15 @@
 Workloads (--config selects, 2 is the default and the
 one the headline metric is quoted on):
 
+  1  MHA decode: 32 heads (32 KV heads), head dim 128, batch 1, 4096 cached
+     tokens, f16 KV head-major contiguous, one split (plan
+     f16_hm_c_g1_u2_d128): the reference's CPU-runnable plumbing case.
   2  Llama-3-8B-shaped GQA decode: 32 query heads over 8 KV heads, head dim
      128, batch 1, 32768 cached tokens, K/V ~ N(0,1) from the reference
      generator (runtime/kvf_host.h:51-61, seed 1) with 1% outlier channels x8,
      quantized int8:G=64 on the GPU by the product's quantize/place kernel,
-     head-major contiguous; plan int8_hm_c_g4_u2_d128, 32 splits.
+     head-major contiguous; plan int8_hm_c_g4_u2_d128, 32 splits. With
+     --fmt f16 the same cache unquantized (plan f16_hm_c_g4_u2_d128).
   3  Paged batched GQA decode: batch 8, lengths uniform in [2048, 8192] (seed
      2), one shared pool of 4096 pages of 16 tokens shuffled with seed 18 and
      handed out in order, token-major int8:64, binary16 query and output,
@@ -16,9 +20,15 @@ one the headline metric is quoted on):
   4  Long-context GQA decode: batch 1, 65536 tokens, int4:G=32 head-major
      contiguous.
 
-One step = one decode-attention call of the plan (the split kernel plus the
-log-sum-exp merge), exactly what the reference's generated kvf_launch_<name>
-enqueues (runtime/kvf_kernels.cuh:309-320).
+One step = one decode-attention call of the plan. Two steps are timed on
+every run and reported in config, their outputs checked to agree before
+timing: the one-launch step (kvf_launch_fused_variant: the split kernel
+merges its splits in its last workgroup per head group) and the drop-in step
+the reference's generated kvf_launch_<name> enqueues (split kernel, then the
+log-sum-exp merge kernel; runtime/kvf_kernels.cuh:309-320). The headline
+value (--step auto) is the one-launch step for uniform lengths and the
+two-launch step for per-sequence lengths (config 3), where the in-kernel
+merge measures slower; --step fused / two-launch picks one.
 
 Timing. The cache is replicated into enough copies that consecutive steps
 never find their bytes in the 256 MiB Infinity Cache (the reference flushes
@@ -57,6 +67,7 @@ HBM_PEAK_GBS = 8000.0
 METRIC = ("\u00b5s/decode step + achieved HBM GB/s (% of peak), "
           "GQA32/8 d128 32k int8:64")
 CONFIG_DEFAULTS = {  # config -> (fmt, group, n, order, block tokens, splits, waves)
+    1: ("f16", 0, 4096, "hm", 0, 1, 4),
     2: ("int8", 64, 32768, "hm", 0, 32, 4),
     3: ("int8", 64, 8192, "tm", 16, 8, 4),
     4: ("int4", 32, 65536, "hm", 0, 32, 8),
@@ -83,9 +94,11 @@ def parse():
                    help="cache replicas rotated over steps (0: enough for 1 GiB)")
     p.add_argument("--cpu-seconds", type=float, default=12.0,
                    help="CPU baseline budget (0 skips it)")
-    p.add_argument("--fused", action="store_true",
-                   help="time the one-launch fused-merge entry point instead of the drop-in "
-                        "two-launch kvf_launch_variant")
+    p.add_argument("--step", default="auto", choices=["auto", "fused", "two-launch"],
+                   help="the step the headline value times: the one-launch kvf_launch_fused_variant, "
+                        "the drop-in two-launch step (split kernel + merge kernel), or auto: "
+                        "one launch for uniform lengths, two launches for per-sequence lengths "
+                        "(config 3, where the in-kernel merge measures slower)")
     p.add_argument("--kv-heads", type=int, default=8, choices=[1, 2, 4, 8],
                    help="KV heads on this GPU, 4 query heads each: 8 is the whole model; 8/P is one "
                         "GPU's share when P GPUs split the heads (no exchange between them)")
@@ -117,7 +130,10 @@ def build_workload(args, R, torch, np):
     dev = torch.device("cuda:0")
     W = types.SimpleNamespace()
     W.B = 8 if args.config == 3 else 1
-    W.H, W.Hkv, W.D = 4 * args.kv_heads, args.kv_heads, 128
+    if args.config == 1:  # MHA: every query head has its own KV head
+        W.H, W.Hkv, W.D = 32, 32, 128
+    else:
+        W.H, W.Hkv, W.D = 4 * args.kv_heads, args.kv_heads, 128
     W.fmt = R.FMT_BY_NAME[args.fmt]
     W.group = args.group if W.fmt != R.FMT_F16 else 0
     W.order = R.ORD_HEAD if args.order == "hm" else R.ORD_TOKEN
@@ -210,6 +226,10 @@ def build_workload(args, R, torch, np):
         W.workload = (f"GQA{H}/{Hkv} d{D} B{B} lengths {int(lens.min())}..{int(lens.max())} "
                       f"(sum {int(lens.sum())}) {args.fmt}:{W.group} {args.order}/paged:{W.bt} "
                       f"pool 4096, f16 q/out")
+    elif args.config == 1:
+        W.data = "synthetic: reference generator seed 1"
+        W.workload = (f"MHA{H} d{D} n{n} B{B} {args.fmt} "
+                      f"{args.order}/{'paged:%d' % W.bt if W.bt else 'contiguous'}")
     else:
         W.data = "synthetic: reference generator seed 1"
         W.workload = (f"GQA{H}/{Hkv} d{D} n{n} B{B} {args.fmt}:{W.group} "
@@ -288,9 +308,10 @@ def main():
     G = W.G
     counters = R.fused_counters(B, Hkv if G > 1 else H)
     cptr = ctypes.c_void_p(counters.data_ptr())
+    cwords = counters.numel()
 
     def step_fused(i):
-        e = L.kvf_launch_fused_variant(vb, refs[i % copies], va, cptr, sh)
+        e = L.kvf_launch_fused_variant(vb, refs[i % copies], va, cptr, cwords, sh)
         if e:
             raise R.KvfError(f"kvf_launch_fused_variant({vid}) failed: {e}")
 
@@ -309,10 +330,10 @@ def main():
     # them; the GPU is held by a spin kernel while the host enqueues ---------
     # the spin lasts about 25 ms per 400 steps, longer than the host takes to
     # enqueue them
-    spin_cycles = int(5e7 * max(1.0, K_ / 400))
-    host_late = []
+    spin_cycles = int(1e8 * max(1.0, K_ / 400))
+    host_late = {}
 
-    def timed(fn):
+    def timed(fn, name):
         e_start = torch.cuda.Event(enable_timing=True)
         e_end = torch.cuda.Event(enable_timing=True)
         torch.cuda.synchronize()
@@ -325,27 +346,28 @@ def main():
         starved = e_start.query()
         torch.cuda.synchronize()
         w1 = time.perf_counter()
-        host_late.append(starved)
+        host_late[name] = bool(starved)
         if starved:
             log("warning: the GPU reached the timed region before the host finished "
                 "enqueueing; the step time includes host launch gaps", quiet=q_)
         return e_start.elapsed_time(e_end) / K_, w1 - w0
 
-    step2_ms, wall_2 = timed(step)
-    fused_ms = timed(step_fused)[0] if S > 1 else None
-    if S > 1 and args.fused:
-        step_ms, wall_t = timed(step_fused)
+    headline_fused = args.step == "fused" or (args.step == "auto" and W.lens is None)
+    step2_ms, wall_2 = timed(step, "two_launch")
+    fused_ms, wall_f = timed(step_fused, "fused") if S > 1 else (None, None)
+    if S > 1 and headline_fused:
+        step_ms, wall_t = fused_ms, wall_f
         path = "kvf_launch_fused_variant (one launch, in-kernel split merge)"
     else:
         step_ms, wall_t = step2_ms, wall_2
         path = ("kvf_launch_varlen_variant" if W.va is not None else "kvf_launch_variant") + \
-            " (split kernel + merge kernel)"
+            (" (split kernel + merge kernel)" if S > 1 else " (one split: one kernel)")
 
     # ---- roofline pass: the same K steps again, each with HIP events bound
     # to its split kernel's own dispatch (the duration a kernel trace reports
     # for that kernel inside the step; the merge launch, if any, follows it as
     # in every step) ---------------------------------------------------------
-    fused_now = S > 1 and args.fused
+    fused_now = S > 1 and headline_fused
     cnt_arg = cptr if fused_now else None
     kev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
            for _ in range(K_)]
@@ -355,7 +377,7 @@ def main():
     torch.cuda.synchronize()
     torch.cuda._sleep(spin_cycles)
     for i in range(K_):
-        e = L.kvf_launch_step_timed(vb, refs[i % copies], va, cnt_arg, sh,
+        e = L.kvf_launch_step_timed(vb, refs[i % copies], va, cnt_arg, cwords if fused_now else 0, sh,
                                     ctypes.c_void_p(kev[i][0].cuda_event),
                                     ctypes.c_void_p(kev[i][1].cuda_event))
         if e:
@@ -368,14 +390,20 @@ def main():
     # persistent step (one launch, workgroups claiming (sequence, head group,
     # split) items from a queue, merge inside): checked against the fused
     # step's output, then timed as the other paths (after the roofline pass,
-    # so the passes before it keep their order in a kernel trace)
+    # so the passes before it keep their order in a kernel trace). The grid
+    # is capped at half the items, so the queue kernel runs and every
+    # workgroup claims (uncapped, a step whose items all fit the resident
+    # grid runs the static fused grid instead)
     persist_ms = None
+    items = S * (Hkv if G > 1 else H) * B
+    persist_wgs = max(1, items // 2)
     if S > 1:
         queue = R.persistent_queue()
         qptr = ctypes.c_void_p(queue.data_ptr())
 
         def step_persistent(i):
-            e = L.kvf_launch_persistent_variant(vb, refs[i % copies], va, cptr, qptr, 0, sh)
+            e = L.kvf_launch_persistent_variant(vb, refs[i % copies], va, cptr, cwords, qptr,
+                                                queue.numel(), persist_wgs, sh)
             if e:
                 raise R.KvfError(f"kvf_launch_persistent_variant({vid}) failed: {e}")
 
@@ -387,7 +415,7 @@ def main():
             raise SystemExit(f"persistent step disagrees with the two-launch step: {relp}")
         for i in range(args.warmup):
             step_persistent(i)
-        persist_ms = timed(step_persistent)[0]
+        persist_ms = timed(step_persistent, "persistent_queue")[0]
 
     alg_bytes = W.alg_bytes
     achieved = alg_bytes / (part_avg_us * 1e-6) / 1e9
@@ -414,7 +442,8 @@ def main():
             "entry_point": path,
             "two_launch_us_per_step": round(step2_ms * 1e3, 3),
             "fused_us_per_step": round(fused_ms * 1e3, 3) if fused_ms is not None else None,
-            "persistent_us_per_step": round(persist_ms * 1e3, 3) if persist_ms is not None else None,
+            "persistent_queue_us_per_step": round(persist_ms * 1e3, 3) if persist_ms is not None else None,
+            "persistent_queue_workgroups": f"{persist_wgs} for {items} items" if persist_ms is not None else None,
             "alg_bytes_per_step": alg_bytes,
             "step_hbm_gbs": round(alg_bytes / (step_ms * 1e-3) / 1e9, 1),
             "step_frac_of_peak": round(alg_bytes / (step_ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
@@ -422,7 +451,7 @@ def main():
             "split_kernel_in_step_us_median": round(part_med_us, 3),
             "cache_copies_rotated": copies,
             "wall_s_timed_region": round(wall_t, 4),
-            "gpu_waited_for_host": any(host_late),
+            "gpu_waited_for_host": host_late,
         },
         "roofline": {
             "bound": "hbm",
@@ -433,6 +462,8 @@ def main():
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 4),
+            "probe_peak": _probe_peak(),
+            "frac_of_probe_peak": round(achieved / _probe_peak(), 4) if _probe_peak() else None,
             "traffic": traffic["hbm_bytes_per_launch"] if traffic else None,
             "traffic_source": traffic["source"] if traffic else None,
         },
@@ -442,6 +473,20 @@ def main():
     if args.cpu_seconds > 0:
         result["cpu_baseline"] = _cpu_baseline(args, W, step_ms, q_)
     print(json.dumps(result), flush=True)
+
+
+def _probe_peak():
+    """bw_peak_gbs of machines/mi355x.gpu: the best HBM read rate the HIP
+    probe measured (kvforge_amd/tools/bw_probe.hip), or None."""
+    try:
+        with open(os.path.join(ROOT, "machines", "mi355x.gpu")) as f:
+            for line in f:
+                k, _, v = line.partition("=")
+                if k.strip() == "bw_peak_gbs":
+                    return float(v)
+    except OSError:
+        pass
+    return None
 
 
 def _traffic_from_profiles(vid, args, alg_bytes):

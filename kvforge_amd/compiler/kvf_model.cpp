@@ -278,7 +278,6 @@ void applyMachineKey(Machine &m, const std::string &key, double value, const std
   else if (key == "lat_mall_ns") m.lat_mall_ns = value;
   else if (key == "bw_copy_gbs") m.bw_copy_gbs = value;
   else if (key == "kernel_floor_us") m.kernel_floor_us = value;
-  else if (key == "round_trip_us") m.round_trip_us = value;
   else throw std::runtime_error("unknown machine key '" + key + "'");
 }
 
@@ -396,8 +395,7 @@ std::string dumpMachine(const Machine &m) {
       << "bw_mall_gbs = " << m.bw_mall_gbs << "\n"
       << "lat_mall_ns = " << m.lat_mall_ns << "\n"
       << "bw_copy_gbs = " << m.bw_copy_gbs << "\n"
-      << "kernel_floor_us = " << m.kernel_floor_us << "\n"
-      << "round_trip_us = " << m.round_trip_us << "\n";
+      << "kernel_floor_us = " << m.kernel_floor_us << "\n";
   }
   return o.str();
 }

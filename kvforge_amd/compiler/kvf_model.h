@@ -159,7 +159,6 @@ struct Machine {
   double lat_mall_ns = 0;
   double bw_copy_gbs = 0;
   double kernel_floor_us = 0;
-  double round_trip_us = 0;
 
   bool cdna() const { return wave_size == 64; }
   double fSmGflops() const { return sms > 0 ? f32_gflops / sms : 0; }

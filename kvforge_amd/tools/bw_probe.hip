@@ -19,8 +19,10 @@
 //           a line no rep has touched: lat_ns. The same hops again behind a
 //           read that clears L2 but not the MALL: lat_mall_ns.
 //   trip    event-bound (hipExtLaunchKernelGGL) duration of a full-chip grid
-//           of empty workgroups, kernel_floor_us, and of one whose lanes each
-//           load 16 bytes of cold memory and store them, round_trip_us.
+//           of empty workgroups, kernel_floor_us, and, printed beside it, of
+//           one whose lanes each load 16 bytes of cold memory and store them
+//           (a kernel's fixed cost hides that round trip; the latency of a
+//           memory round trip is the chase's lat_ns).
 //   cached  repeated reads of a set that fits one XCD's L2 and of one that
 //           fits the MALL: bw_l2_gbs, bw_mall_gbs.
 //   grain   one dword per S bytes of cold memory: bytes each access costs at
@@ -514,7 +516,6 @@ int main(int argc, char **argv) {
   std::fprintf(f, "lat_mall_ns = %.0f\n", lat_mall);
   std::fprintf(f, "bw_copy_gbs = %.0f\n", bw_copy);
   std::fprintf(f, "kernel_floor_us = %.2f\n", floor_us);
-  std::fprintf(f, "round_trip_us = %.2f\n", trip_us);
   if (!resources.empty()) std::fprintf(f, "resources = %s\n", resources.c_str());
   if (f != stdout) {
     std::fclose(f);

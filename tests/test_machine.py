@@ -34,7 +34,7 @@ def _check(m):
     assert f("bw_sm_gbs") * 20 < f("bw_peak_gbs")
     assert f("bw_copy_gbs") <= 8000 and f("bw_l2_gbs") > f("bw_peak_gbs")
     assert int(m["sector_bytes"]) in (64, 128)
-    assert f("round_trip_us") >= f("kernel_floor_us") > 0
+    assert f("kernel_floor_us") > 0 and "round_trip_us" not in m
 
 
 def test_committed_machine_file():
