@@ -727,16 +727,16 @@ __device__ __forceinline__ void decode_item(const Args &a, const Ext &x, const i
       l_sum *= alpha;
 #pragma unroll
       for (int p = 0; p < PASSES; ++p) zacc[p] *= alpha;
+      // accumulator row 4r+i belongs to head (4r+i) mod G: take that
+      // column's alpha; whole float4 accumulators are scaled, so each keeps
+      // its registers (per-element products were moved back at every tile)
+      float4_t a4;
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        // accumulator row 4r+i belongs to head (4r+i) mod G: take that
-        // column's alpha
-        const float ai = __shfl(alpha, 16 * r + ((4 * r + i) & 15));
+      for (int i = 0; i < 4; ++i) a4[i] = __shfl(alpha, 16 * r + ((4 * r + i) & 15));
 #pragma unroll
-        for (int p = 0; p < PASSES; ++p)
+      for (int p = 0; p < PASSES; ++p)
 #pragma unroll
-          for (int e = 0; e < EV; ++e) acc[p][e][i] *= ai;
-      }
+        for (int e = 0; e < EV; ++e) acc[p][e] = acc[p][e] * a4;
       m_run = cand;
       m_neg = -cand * UNIT;
     }
@@ -805,27 +805,42 @@ __device__ __forceinline__ void decode_item(const Args &a, const Ext &x, const i
   };
 
   // ---- main loop: ring of DEPTH tiles ------------------------------------------
-  // Steady state: every step issues the real tile DEPTH-1 ahead and consumes
-  // one. The last DEPTH-1 tiles are consumed after the loop without issuing
-  // anything, so no zero-length loads are left in flight at the end of the
-  // stream for the epilogue to wait on.
+  // Every step issues the tile DEPTH-1 ahead and consumes one; tile k sits in
+  // ring slot k % DEPTH. Whole rounds of DEPTH steps run with no exit inside a
+  // round (the accumulators then stay in their registers across the loop;
+  // early exits between steps made the compiler copy them at every tile),
+  // then up to DEPTH-1 single steps. The last DEPTH-1 tiles are consumed
+  // after the loop without issuing anything (the drain below), so no
+  // zero-length loads are left in flight for the epilogue to wait on.
+  // Masking: the drain holds the split's last tile, the only one that may end
+  // past t1; split tile 0 starts before t0 only when t0 is not a multiple of
+  // the tile, and then (the one case) every step of the loop is masked.
+  // (Scheduling barriers keep each step's loads ahead of its compute.)
   int k = 0;
-  bool streaming = true;
-  while (streaming) {
-    static_for<DEPTH>([&](auto Ui) __attribute__((always_inline)) {
-      constexpr int u = decltype(Ui)::value;
-      if (!streaming) return;
-      if (k + DEPTH - 1 >= nk) {
-        streaming = false;
-        return;
+  auto stream = [&](auto mask_tag) __attribute__((always_inline)) {
+    while (k + 2 * DEPTH - 1 <= nk) {
+      static_for<DEPTH>([&](auto Ui) __attribute__((always_inline)) {
+        constexpr int s = decltype(Ui)::value;
+        __builtin_amdgcn_sched_barrier(0);
+        issue(ring(std::integral_constant<int, (s + DEPTH - 1) % DEPTH>{}), k + DEPTH - 1);
+        __builtin_amdgcn_sched_barrier(0);
+        compute(ring(Ui), k, mask_tag);
+        ++k;
+      });
+    }
+    static_for<DEPTH - 1>([&](auto Ui) __attribute__((always_inline)) {
+      constexpr int s = decltype(Ui)::value;
+      if (k + DEPTH - 1 < nk) { // a prefix of the steps: once false, k stays put
+        __builtin_amdgcn_sched_barrier(0);
+        issue(ring(std::integral_constant<int, (s + DEPTH - 1) % DEPTH>{}), k + DEPTH - 1);
+        __builtin_amdgcn_sched_barrier(0);
+        compute(ring(Ui), k, mask_tag);
+        ++k;
       }
-      issue(ring(std::integral_constant<int, (u + DEPTH - 1) % DEPTH>{}), k + DEPTH - 1);
-      const int tbase = (tile0 + tstep * (wave + nw * k)) * TT;
-      if (tbase >= t0 && tbase + TT <= t1) compute(ring(Ui), k, std::false_type{});
-      else compute(ring(Ui), k, std::true_type{});
-      ++k;
     });
-  }
+  };
+  if (t0 % TT == 0) stream(std::false_type{});
+  else stream(std::true_type{});
   // persistent step: thread 0 claims the workgroup's next item behind the
   // last tiles' loads, so the claim's round trip overlaps the drain
   unsigned claim = 0;
