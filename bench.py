@@ -315,12 +315,17 @@ def main():
         if e:
             raise R.KvfError(f"kvf_launch_fused_variant({vid}) failed: {e}")
 
+    # the two merges fold the same partials in different orders: fp32 outputs
+    # agree to 1e-5; binary16 outputs (config 3) may round a few elements to
+    # neighbouring values, each at most 2^-11 relative
+    agree = 1e-5 if W.va is None else 2.0 ** -11
+    relf = None
     if S > 1:
         out_t.zero_()
         step_fused(0)
         torch.cuda.synchronize()
         relf = float(torch.linalg.vector_norm(got - out_t.float()) / torch.linalg.vector_norm(got))
-        if not (relf < 1e-5 and int(counters.abs().sum()) == 0):
+        if not (relf < agree and int(counters.abs().sum()) == 0):
             raise SystemExit(f"fused step disagrees with the two-launch step: {relf}")
         for i in range(args.warmup):
             step_fused(i)
@@ -411,7 +416,7 @@ def main():
         step_persistent(0)
         torch.cuda.synchronize()
         relp = float(torch.linalg.vector_norm(got - out_t.float()) / torch.linalg.vector_norm(got))
-        if not (relp < 1e-5 and int(counters.abs().sum()) == 0 and int(queue.abs().sum()) == 0):
+        if not (relp < agree and int(counters.abs().sum()) == 0 and int(queue.abs().sum()) == 0):
             raise SystemExit(f"persistent step disagrees with the two-launch step: {relp}")
         for i in range(args.warmup):
             step_persistent(i)
@@ -442,6 +447,7 @@ def main():
             "entry_point": path,
             "two_launch_us_per_step": round(step2_ms * 1e3, 3),
             "fused_us_per_step": round(fused_ms * 1e3, 3) if fused_ms is not None else None,
+            "fused_vs_two_launch_rel_l2": float(f"{relf:.3g}") if relf is not None else None,
             "persistent_queue_us_per_step": round(persist_ms * 1e3, 3) if persist_ms is not None else None,
             "persistent_queue_workgroups": f"{persist_wgs} for {items} items" if persist_ms is not None else None,
             "alg_bytes_per_step": alg_bytes,

@@ -815,15 +815,15 @@ __device__ __forceinline__ void decode_item(const Args &a, const Ext &x, const i
   // Masking: the drain holds the split's last tile, the only one that may end
   // past t1; split tile 0 starts before t0 only when t0 is not a multiple of
   // the tile, and then (the one case) every step of the loop is masked.
-  // (Scheduling barriers keep each step's loads ahead of its compute.)
+  // Inside a round the compiler schedules loads and compute freely (barriers
+  // there cost 3 % on int4:32 and 6 % on long variable-length contiguous
+  // batches); the single steps keep each step's loads ahead of its compute.
   int k = 0;
   auto stream = [&](auto mask_tag) __attribute__((always_inline)) {
     while (k + 2 * DEPTH - 1 <= nk) {
       static_for<DEPTH>([&](auto Ui) __attribute__((always_inline)) {
         constexpr int s = decltype(Ui)::value;
-        __builtin_amdgcn_sched_barrier(0);
         issue(ring(std::integral_constant<int, (s + DEPTH - 1) % DEPTH>{}), k + DEPTH - 1);
-        __builtin_amdgcn_sched_barrier(0);
         compute(ring(Ui), k, mask_tag);
         ++k;
       });

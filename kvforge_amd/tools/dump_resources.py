@@ -18,9 +18,11 @@ wavefronts per workgroup; `occupancy` is the compiler's waves per SIMD.
 
 valu, mfma, lds, salu: instructions per 32-token tile of the kernel's main
 loop, counted in the gfx950 assembly of the same compile (-S): the loop is
-the one holding the most MFMAs in its own blocks; its blocks hold the tile's compute
-once per code path (masked and unmasked copies, one per unrolled step), so
-the counts are divided by (MFMAs in the loop / MFMAs per tile). MFMAs per
+the one holding the most MFMAs in its own blocks (the main loop comes in a
+masked and an unmasked copy, one for chunks that start inside a tile; the
+unmasked one, with fewer vector instructions, is taken); its blocks hold the
+tile's compute once per unrolled step, so the counts are divided by (MFMAs
+in the loop / MFMAs per tile). MFMAs per
 tile follow from the kernel's column geometry: COLS = g x (d / group) query
 columns (g for f16), two passes when COLS > 16, hi and lo in one MFMA when
 COLS <= 8, and per pass and binary16 half 2 x d/32 QK steps plus d/16 PV
@@ -62,7 +64,8 @@ def mfma_per_tile(fmt, d, group, g):
 
 
 def loop_mix(lines):
-    """Instruction mix of the loop with the most MFMAs in its own blocks. A
+    """Instruction mix of the loop with the most MFMAs in its own blocks (the
+    fewest vector instructions breaking a tie). A
     block (a `.LBB` label or an unlabelled `; %bb.N:` fall-through) counts for
     the innermost loop holding it, as the assembler's comments on the block's
     first lines name it ("Loop Header: Depth=d" for a header, "in Loop:
@@ -97,7 +100,11 @@ def loop_mix(lines):
             loops.setdefault(owner, []).extend(blocks[b])
     if not loops:
         return None
-    ops = max(loops.values(), key=lambda o: sum(x.startswith("v_mfma") for x in o))
+    # of several loops with that many MFMAs (the main loop's masked and
+    # unmasked copies), the one with the fewest vector ALU instructions: the
+    # unmasked copy, which every chunk starting on a tile boundary runs
+    ops = max(loops.values(), key=lambda o: (sum(x.startswith("v_mfma") for x in o),
+                                             -sum(x.startswith("v_") for x in o)))
     mix = {"mfma": 0, "valu": 0, "lds": 0, "salu": 0}
     for op in ops:
         if op.startswith("v_mfma"):
