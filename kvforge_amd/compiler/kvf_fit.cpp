@@ -252,9 +252,12 @@ Calib calibrate(const std::vector<SweepRow> &rows, const Machine &m, const Calib
   };
   Calib best = start;
   if (m.cdna()) {
-    // the CDNA form's own constants (per-CU stream rate, spill cost)
+    // the CDNA form's own constants (per-CU stream rate, spill cost, merge round trip,
+    // scalar issue weight)
     knobs.push_back({&Calib::cu_frac, 0.1, 1.5, false});
     knobs.push_back({&Calib::spill_cost, 0.0, 4.0, false});
+    knobs.push_back({&Calib::merge_trip, 0.0, 32.0, false});
+    knobs.push_back({&Calib::salu_w, 0.0, 1.0, false});
     best.cdna = true;
   }
   double best_loss = loss(best);

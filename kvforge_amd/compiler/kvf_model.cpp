@@ -441,8 +441,8 @@ Calib loadCalib(const std::filesystem::path &p) {
     const double v = std::stod(raw);
     if (k.rfind("rel_err.", 0) == 0) {
       c.rel_err[k.substr(8)] = v;
-    } else if (k == "cu_frac" || k == "spill_cost") {
-      (k == "cu_frac" ? c.cu_frac : c.spill_cost) = v;
+    } else if (k == "cu_frac" || k == "spill_cost" || k == "merge_trip" || k == "salu_w") {
+      (k == "cu_frac" ? c.cu_frac : k == "spill_cost" ? c.spill_cost : k == "merge_trip" ? c.merge_trip : c.salu_w) = v;
       c.cdna = true;
     } else {
       calibScalar(c, k) = v;
@@ -456,7 +456,9 @@ std::string dumpCalib(const Calib &c) {
   o << std::setprecision(8);
   Calib t = c;
   for (const char *k : calibScalarKeys()) o << k << " = " << calibScalar(t, k) << "\n";
-  if (c.cdna) o << "cu_frac = " << c.cu_frac << "\nspill_cost = " << c.spill_cost << "\n";
+  if (c.cdna)
+    o << "cu_frac = " << c.cu_frac << "\nspill_cost = " << c.spill_cost << "\nmerge_trip = " << c.merge_trip
+      << "\nsalu_w = " << c.salu_w << "\n";
   for (const auto &kv : c.rel_err) o << "rel_err." << kv.first << " = " << kv.second << "\n";
   return o.str();
 }
@@ -670,11 +672,17 @@ Cost warpEvaluate(const DecodeSpec &s, const Machine &m, const Calib &c, const P
 //              more waves share it (one's MFMAs run under another's VALU);
 //              spills (scratch bytes per lane) costing spill_cost per 64 B.
 //              The counts are the compiled loop's own (resource table
-//              columns valu, mfma, lds) where the table has them, else the
-//              estimate of cdnaTile
-//   fixed      launch_frac and merge_frac (second kernel) of launch_us, plus
-//              warp_w0 loaded latencies per round of workgroups (query load,
-//              first tile, wave combine and partial write)
+//              columns valu, mfma, lds, and salu weighted salu_w) where the
+//              table has them, else the estimate of cdnaTile
+//   fixed      launch_frac of launch_us, plus warp_w0 loaded latencies per
+//              round of workgroups (query load, first tile, wave combine and
+//              partial write)
+//   merge      the second kernel: merge_frac of launch_us, then one
+//              workgroup per (sequence, query head) folding its S partial
+//              rows in chunks of 32, 1, 2, 4 or 8 chunks side by side
+//              (kvf_merge.hip), so ceil(chunks / slices) round trips of
+//              merge_trip * lat_ns, and the rows streamed at one
+//              workgroup's rate (cu_frac * bw_sm)
 //   paging     c_page_ns per page a workgroup walks, per round
 struct CdnaTile {
   int depth = 2;     // ring of tiles per wave
@@ -735,8 +743,9 @@ Cost cdnaEvaluate(const DecodeSpec &s, const Machine &m, const Calib &c, const P
   const Machine::KernelRes kr = cdnaResources(m, s, p, G, t);
   if (kr.mfma > 0) {
     // the compiled loop's own counts replace the estimate; a cross-row
-    // shuffle through LDS occupies an issue slot like a VALU instruction
-    t.valu = kr.valu + kr.lds;
+    // shuffle through LDS occupies an issue slot like a VALU instruction, a
+    // scalar instruction salu_w of one
+    t.valu = kr.valu + kr.lds + c.salu_w * kr.salu;
     t.mfma = 16.0 * kr.mfma / 4.0;
   }
 
@@ -807,7 +816,14 @@ Cost cdnaEvaluate(const DecodeSpec &s, const Machine &m, const Calib &c, const P
 
   // fill: the bytes requested at the start queue at peak bandwidth
   const double t_fill = conc * bif_wg / (peak * 1000.0);
-  if (p.part.splits > 1) k.t_merge_us = c.merge_frac * m.launch_us + k.partial_bytes / (l2 * 1000.0);
+  if (p.part.splits > 1) {
+    const int chunks = (p.part.splits + 31) / 32;
+    const int slices = chunks <= 1 ? 1 : chunks == 2 ? 2 : chunks <= 4 ? 4 : 8;
+    const double trips = std::ceil(static_cast<double>(chunks) / slices);
+    const double wg_rows = 4.0 * p.part.splits * (s.d + 2);
+    k.t_merge_us = c.merge_frac * m.launch_us + trips * c.merge_trip * m.lat_ns / 1000.0 +
+                   wg_rows / (c.cu_frac * m.bw_sm_gbs * 1000.0);
+  }
   if (p.layout.paged() && p.layout.block_tokens > 0)
     k.t_page_us = rounds * std::ceil(chunk_max / p.layout.block_tokens) * c.c_page_ns / 1000.0;
   k.t_launch_us = c.launch_frac * m.launch_us + c.warp_w0 * lat_us * rounds + t_fill;

@@ -194,6 +194,12 @@ struct Calib {
   // file for a 32-lane-warp machine keeps the reference's keys exactly.
   double cu_frac = 0.6;
   double spill_cost = 0.5;
+  // CDNA form only: one memory round trip of the merge kernel, in units of
+  // the machine's lat_ns (the merge runs after the stream, on a quiet memory)
+  double merge_trip = 1.5;
+  // CDNA form only: issue slots a scalar instruction of the main loop takes
+  // from its wave (address and page-table arithmetic, loop control)
+  double salu_w = 0.0;
   bool cdna = false;
   std::map<std::string, double> rel_err;
   static Calib defaults();
