@@ -26,9 +26,9 @@ timing: the one-launch step (kvf_launch_fused_variant: the split kernel
 merges its splits in its last workgroup per head group) and the drop-in step
 the reference's generated kvf_launch_<name> enqueues (split kernel, then the
 log-sum-exp merge kernel; runtime/kvf_kernels.cuh:309-320). The headline
-value (--step auto) is the one-launch step for uniform lengths and the
-two-launch step for per-sequence lengths (config 3), where the in-kernel
-merge measures slower; --step fused / two-launch picks one.
+value (--step auto) is the faster of the two in this run: they are within a
+few per cent of each other and which one wins differs between boxes;
+config.entry_point names it, and --step fused / two-launch fixes one.
 
 Timing. The cache is replicated into enough copies that consecutive steps
 never find their bytes in the 256 MiB Infinity Cache (the reference flushes
@@ -97,8 +97,7 @@ def parse():
     p.add_argument("--step", default="auto", choices=["auto", "fused", "two-launch"],
                    help="the step the headline value times: the one-launch kvf_launch_fused_variant, "
                         "the drop-in two-launch step (split kernel + merge kernel), or auto: "
-                        "one launch for uniform lengths, two launches for per-sequence lengths "
-                        "(config 3, where the in-kernel merge measures slower)")
+                        "the faster of the two in this run (both are timed either way)")
     p.add_argument("--kv-heads", type=int, default=8, choices=[1, 2, 4, 8],
                    help="KV heads on this GPU, 4 query heads each: 8 is the whole model; 8/P is one "
                         "GPU's share when P GPUs split the heads (no exchange between them)")
@@ -357,9 +356,12 @@ def main():
                 "enqueueing; the step time includes host launch gaps", quiet=q_)
         return e_start.elapsed_time(e_end) / K_, w1 - w0
 
-    headline_fused = args.step == "fused" or (args.step == "auto" and W.lens is None)
     step2_ms, wall_2 = timed(step, "two_launch")
     fused_ms, wall_f = timed(step_fused, "fused") if S > 1 else (None, None)
+    # auto: whichever of the two entry points ran faster on this GPU (both are
+    # product paths; which one wins differs between boxes by a few per cent)
+    headline_fused = args.step == "fused" or (args.step == "auto" and fused_ms is not None
+                                              and fused_ms < step2_ms)
     if S > 1 and headline_fused:
         step_ms, wall_t = fused_ms, wall_f
         path = "kvf_launch_fused_variant (one launch, in-kernel split merge)"

@@ -818,6 +818,16 @@ __device__ __forceinline__ void decode_item(const Args &a, const Ext &x, const i
   // Inside a round the compiler schedules loads and compute freely (barriers
   // there cost 3 % on int4:32 and 6 % on long variable-length contiguous
   // batches); the single steps keep each step's loads ahead of its compute.
+  // Binary16 rows with 4 waves and a ring of 2 take the per-step form instead
+  // (an exit test before every step, each step masked only where its tile
+  // crosses [t0, t1)): it compiles to 248 VGPRs against 255 plus 20 AGPRs for
+  // whole rounds, which keeps two 4-wave workgroups per CU (2 % faster at GQA
+  // 32/8 n32768 f16, 10 % on a batch of 16 sequences that needs several
+  // rounds of workgroups); with 8 waves or a ring of 3 it measured slower
+  // (median 1.3-1.8x over the f16 plans of the uniform sweep). (The per-step
+  // loop is written inline below: wrapped in a lambda it compiled to 256
+  // VGPRs plus 86 AGPRs.)
+  constexpr bool PER_STEP = FMT == FMT_F16 && DEPTH == 2 && WPB == 4;
   int k = 0;
   auto stream = [&](auto mask_tag) __attribute__((always_inline)) {
     while (k + 2 * DEPTH - 1 <= nk) {
@@ -839,7 +849,24 @@ __device__ __forceinline__ void decode_item(const Args &a, const Ext &x, const i
       }
     });
   };
-  if (t0 % TT == 0) stream(std::false_type{});
+  if constexpr (PER_STEP) {
+    bool streaming = true;
+    while (streaming) {
+      static_for<DEPTH>([&](auto Ui) __attribute__((always_inline)) {
+        constexpr int u = decltype(Ui)::value;
+        if (!streaming) return;
+        if (k + DEPTH - 1 >= nk) {
+          streaming = false;
+          return;
+        }
+        issue(ring(std::integral_constant<int, (u + DEPTH - 1) % DEPTH>{}), k + DEPTH - 1);
+        const int tbase = (tile0 + tstep * (wave + nw * k)) * TT;
+        if (tbase >= t0 && tbase + TT <= t1) compute(ring(Ui), k, std::false_type{});
+        else compute(ring(Ui), k, std::true_type{});
+        ++k;
+      });
+    }
+  } else if (t0 % TT == 0) stream(std::false_type{});
   else stream(std::true_type{});
   // persistent step: thread 0 claims the workgroup's next item behind the
   // last tiles' loads, so the claim's round trip overlaps the drain

@@ -1,6 +1,6 @@
 """Per-phase timeline of one decode step on the GPU, from per-wave clock stamps.
 
-    python kvforge_amd/tools/timeline.py [--config 2] [--steps 60] [--out FILE.md] [--raw FILE.npz]
+    python kvforge_amd/tools/timeline.py [--config 2] [--order hm|tm] [--steps 60] [--out FILE.md] [--raw FILE.npz]
 
 Builds, under kvforge_amd/_build/timeline/, a copy of the library that holds
 only the benchmarked plan of the chosen bench.py config, with s_memrealtime
@@ -78,7 +78,10 @@ def _patches():
          "  return fx(*a, x, Launch{}, st);"),
         ("kvf_kernels.hpp", "  constexpr int nw = WPB; // equals a.warps, checked at launch\n",
          "  constexpr int nw = WPB; // equals a.warps, checked at launch\n" + tsdef +
-         "  " + _stamp(0, "lane") + "\n"),
+         "  " + _stamp(0, "lane") + "\n"
+         # slot 7: where the wave runs (XCC_ID in the high word, HW_ID: CU, SIMD, wave slot)
+         "  TS(7, ((unsigned long long)__builtin_amdgcn_s_getreg(0x1814) << 32) |\n"
+         "        (unsigned)__builtin_amdgcn_s_getreg(0xF804));\n"),
         ("kvf_kernels.hpp", "        compute(ring(Ui), k, mask_tag);\n        ++k;\n      });\n    }",
          "        compute(ring(Ui), k, mask_tag);\n        if (k == 0) " + _stamp(1, "acc[0][0][0]") +
          "\n        ++k;\n      });\n    }"),
@@ -187,6 +190,8 @@ def _pct(x, q):
 def main():
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--config", type=int, default=2, choices=[2, 3, 4])
+    ap.add_argument("--order", default=None, choices=["hm", "tm"],
+                    help="KV order instead of the config's (the same data, placed the other way)")
     ap.add_argument("--steps", type=int, default=60)
     ap.add_argument("--out", default=None)
     ap.add_argument("--raw", default=None)
@@ -197,6 +202,7 @@ def main():
     from kvforge_amd import runtime as R
 
     fmt, group, n, order, bt, splits, waves = bench.CONFIG_DEFAULTS[a0.config]
+    order = a0.order or order
     args = types.SimpleNamespace(config=a0.config, fmt=fmt, group=group, n=n, order=order, block_tokens=bt,
                                  copies=0, unroll=2, pack=1, splits=splits, warps=waves, kv_heads=8,
                                  varlen_flags=0)
@@ -287,6 +293,7 @@ def main():
     lines = [f"# Timeline of one decode step: {W.workload}, plan {W.vid} splits={S} waves={waves}", "",
              "Command (repository root on the GPU box):", "",
              f"    python3 kvforge_amd/tools/timeline.py --config {a0.config} --steps {a0.steps}"
+             + (f" --order {a0.order}" if a0.order else "")
              + (f" --out {a0.out}" if a0.out else ""), "",
              "One-launch step (kvf_launch_fused_variant), per-wave s_memrealtime stamps (10 ns), times "
              "in us after the step's first wave started, over the steps after the first five; "
@@ -310,7 +317,9 @@ def main():
         with open(a0.out, "w") as fh:
             fh.write(text + "\n")
     if a0.raw:
-        np.savez_compressed(a0.raw, t=t, empty=et)
+        # t[step][wave][slot]: wave w of workgroup (split, head group, sequence)
+        # = w // waves in (x, y, z) grid order; slot 7 holds XCC_ID << 32 | HW_ID
+        np.savez_compressed(a0.raw, t=t, empty=et, grid=np.array([S, W.Hkv, W.B, waves]))
 
 
 if __name__ == "__main__":
