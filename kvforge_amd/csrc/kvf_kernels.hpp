@@ -96,6 +96,20 @@ constexpr float SUB_UNIT = 16777216.f;   // 2^24: undoes the subnormal encoding 
 constexpr float LO_SCALE = 2048.f;       // 2^11: lo half of a packed softmax weight
 constexpr float LO_INV = 1.f / 2048.f;
 constexpr float INT4_HI = 16.f;          // high nibbles enter the MFMAs as code * 16
+// A quantized kernel's query enters its binary16 hi/lo split multiplied by
+// 2^6: the lo half of an element below 4 (in log2 units per score) would be
+// a binary16 subnormal, which keeps fewer bits (int4 high-nibble slots, held
+// at 1/16, most of all). Scores come out 2^6 larger, which the score unit
+// takes back. The query must then stay below 1023 in magnitude after the
+// softmax scale (|q| < 8000 at d = 128 with scale 1/sqrt(d)).
+constexpr float Q_PRESCALE = 64.f;
+// int8 kernels whose weights share one accumulator for hi and lo (more than
+// 8 columns) take softmax weights 2^4 larger: p * scale_v is far below 1 and
+// its lo half would otherwise be subnormal. The factor is undone in the
+// wave's running max (m - 4 for l and O that are 16 times larger), so it
+// costs nothing per tile. It bounds an int8 V group's scale at 16 (a range
+// of 4080 per group) instead of 256: a weight never exceeds 2^(8+4) * scale.
+constexpr float W_LOG2 = 4.f;
 // V codes enter the PV MFMA centred on their mid-range, code - mid, and a
 // token's zero point becomes zero + mid * scale: the products and the zero
 // sum then stay near the output's own magnitude instead of cancelling (int8
@@ -339,7 +353,9 @@ __device__ __forceinline__ void decode_item(const Args &a, const Ext &x, const i
   constexpr int DEPTH = depth_of<U>();
   constexpr bool HL_LDS = HL && hl_lds_fits<D, G>(WPB);
   constexpr int NQ = HL ? 1 : 2;                   // query operands per k-step
-  constexpr float UNIT = QUANT ? SUB_UNIT : 1.f; // log2 units per score unit
+  constexpr float UNIT = QUANT ? SUB_UNIT / Q_PRESCALE : 1.f; // log2 units per score unit
+  constexpr float QPS = QUANT ? Q_PRESCALE : 1.f;
+  constexpr float WOFF = FMT == FMT_INT8 && !HL ? W_LOG2 : 0.f; // log2 of the weights' extra factor
   constexpr float TAU_S = TAU / UNIT;
   using Buf = TileBuf<FMT, D, GQ, G>;
 
@@ -581,7 +597,7 @@ __device__ __forceinline__ void decode_item(const Args &a, const Ext &x, const i
         for (int i = 0; i < 8; ++i) {
           const float v = mine ? raw[ks][slot_elem<FMT>(i)] * a.scale_log2 : 0.f;
           // int4: slots 4-7 meet high nibbles entered as code * 16
-          const float vb = FMT == FMT_INT4 && i >= 4 ? v * (1.f / INT4_HI) : v;
+          const float vb = FMT == FMT_INT4 && i >= 4 ? v * (QPS / INT4_HI) : v * QPS;
           const _Float16 hi = (_Float16)vb;
           const _Float16 lo = (_Float16)(vb - (float)hi);
           if constexpr (HL) {
@@ -608,7 +624,7 @@ __device__ __forceinline__ void decode_item(const Args &a, const Ext &x, const i
 #pragma unroll
   for (int p = 0; p < PASSES; ++p) zacc[p] = 0.f;
   float m_run = -INFINITY;  // running max, score units; equal across a head's lanes
-  float m_neg = INFINITY;   // -m_run in log2 units
+  float m_neg = INFINITY;   // -m_run in log2 units, plus WOFF
   float m_true = -INFINITY; // exact max of this lane's scores, score units
   float l_sum = 0.f;
 
@@ -730,8 +746,13 @@ __device__ __forceinline__ void decode_item(const Args &a, const Ext &x, const i
       for (int mask = G; mask < 16; mask <<= 1) cand = fmaxf(cand, __shfl_xor(cand, mask));
       cand = fmaxf(cand, xor16(cand));
       cand = fmaxf(cand, xor32(cand));
-      const float alpha =
-          cand == -INFINITY ? 1.f : __builtin_amdgcn_exp2f((m_run - cand) * UNIT);
+      // the running max moves on a grid of 2^-8 log2 units (rounded up), so
+      // the offsets taken from it are exact: m_neg with WOFF, the rescale
+      // factor and the wave's stored max. A rounding there would be one
+      // factor shared by every weight of a rescale epoch or of a wave's
+      // partial, which no later sum averages out.
+      const float cl2 = ceilf(cand * (UNIT * 256.f)) * (1.f / 256.f);
+      const float alpha = cand == -INFINITY ? 1.f : __builtin_amdgcn_exp2f(fmaf(m_run, UNIT, -cl2));
       l_sum *= alpha;
 #pragma unroll
       for (int p = 0; p < PASSES; ++p) zacc[p] *= alpha;
@@ -745,8 +766,8 @@ __device__ __forceinline__ void decode_item(const Args &a, const Ext &x, const i
       for (int p = 0; p < PASSES; ++p)
 #pragma unroll
         for (int e = 0; e < EV; ++e) acc[p][e] = acc[p][e] * a4;
-      m_run = cand;
-      m_neg = -cand * UNIT;
+      m_run = cl2 * (1.f / UNIT);
+      m_neg = WOFF - cl2;
     }
     float pj[8];
 #pragma unroll
@@ -911,7 +932,7 @@ __device__ __forceinline__ void decode_item(const Args &a, const Ext &x, const i
   float *sM = smem + nw * G * D;
   float *sL = sM + nw * G * 3;
   if (r == 0 && c < G) {
-    sM[(wave * G + c) * 3 + 0] = m_run * UNIT;
+    sM[(wave * G + c) * 3 + 0] = fmaf(m_run, UNIT, -WOFF);
     sM[(wave * G + c) * 3 + 1] = l_sum;
     sM[(wave * G + c) * 3 + 2] = m_true * UNIT;
   }
