@@ -45,6 +45,9 @@ its own dispatch. A third pass repeats the second with events created
 without the system-scope fence (hipEventDisableSystemFence), which otherwise
 ends each timed dispatch with a system-scope release; it is reported beside
 the roofline (config.split_kernel_in_step_us_avg_events_without_fence).
+config.reference_method_us_median times the step as the reference's harness
+does (runtime/kvf_host.h:302-331): one step per rep after a cache flush,
+event-timed, median of 100 reps.
 
 The CPU baseline times the oracle's restatement of reference_attention
 (runtime/kvf_host.h:202-234, double precision) on the same dequantised cache,
@@ -433,6 +436,27 @@ def main():
             step_persistent(i)
         persist_ms = timed(step_persistent, "persistent_queue")[0]
 
+    # the reference's own timing method (runtime/kvf_host.h:302-331): one
+    # step of the headline entry point per rep, event-timed, each after a
+    # flush, median over the reps. The flush reads 1 GiB, which evicts L2 and
+    # the 256 MiB MALL (the reference writes its flush buffer; a read leaves
+    # no dirty lines to be written back while the step runs)
+    step_ref = step_fused if headline_fused else step
+    flush = torch.ones(1 << 28, dtype=torch.float32, device="cuda:0")
+    sink = torch.empty((), dtype=torch.float32, device="cuda:0")
+    ref_reps = 100
+    rev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+           for _ in range(ref_reps)]
+    torch.cuda.synchronize()
+    for i in range(ref_reps):
+        torch.sum(flush, dim=0, out=sink)
+        rev[i][0].record(st)
+        step_ref(i)
+        rev[i][1].record(st)
+    torch.cuda.synchronize()
+    ref_method_us = 1e3 * statistics.median(e0.elapsed_time(e1) for e0, e1 in rev)
+    del flush, sink
+
     alg_bytes = W.alg_bytes
     achieved = alg_bytes / (part_avg_us * 1e-6) / 1e9
     traffic = _traffic_from_profiles(vid, args, W.alg_bytes)
@@ -467,6 +491,9 @@ def main():
             "split_kernel_in_step_us_avg": round(part_avg_us, 3),
             "split_kernel_in_step_us_median": round(part_med_us, 3),
             "split_kernel_in_step_us_avg_events_without_fence": round(nofence_avg_us, 3),
+            "reference_method_us_median": round(ref_method_us, 3),
+            "reference_method": f"one step per rep after a 1 GiB read, event-timed, median of {ref_reps} "
+                                "(runtime/kvf_host.h:302-331)",
             "cache_copies_rotated": copies,
             "wall_s_timed_region": round(wall_t, 4),
             "gpu_waited_for_host": host_late,
