@@ -4,9 +4,10 @@
 // This translation unit is built with -amdgpu-kernarg-preload-count=10: the
 // merge kernels' arguments (two partial-buffer pointers, two output pointers,
 // H, splits: 10 dwords) arrive in SGPRs when the wave starts, so its first
-// loads do not wait for the kernel-argument segment. The split kernels are
-// built without it (their Args block does not fit, and preloading its first
-// fields measured no gain). Measured on MI355X (three alternating rounds), the
+// loads do not wait for the kernel-argument segment. (The split kernels take
+// the fields their first loads need as 14 leading dwords ahead of Args, built
+// with a preload count of 14; preloading Args' own first fields, pointers
+// only, had measured no gain.) Measured on MI355X (three alternating rounds), the
 // decode step went from 9.02 to 8.73 us at n = 4096 and from 18.40 to 18.18 us
 // at GQA 32/8, d128, n 32768, int8:64, 32 splits.
 #include "kvf_kernels.hpp"

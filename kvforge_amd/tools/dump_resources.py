@@ -43,7 +43,7 @@ ROOT = os.path.dirname(PKG)
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 FLAGS = ["-std=c++17", "-O3", "--offload-arch=gfx950", "-fPIC", "-Xclang", "-target-feature",
          "-Xclang", "-packed-fp32-ops", "-mllvm", "-amdgpu-mfma-vgpr-form",
-         "-mllvm", "-amdgpu-atomic-optimizer-strategy=None",
+         "-mllvm", "-amdgpu-atomic-optimizer-strategy=None", "-mllvm", "-amdgpu-kernarg-preload-count=14",
          "-I" + os.path.join(ROOT, "include"),
          "-I" + os.path.join(PKG, "csrc"), "-Rpass-analysis=kernel-resource-usage"]
 NAME = re.compile(r"decode_partialILi(\d+)ELi(\d+)ELi(\d+)ELi(\d+)ELi(\d+)ELi(\d+)ELb(\d)ELi(\d+)E")

@@ -163,7 +163,8 @@ def build(vid, inst):
     objs = []
     for name in ("kvf_runtime", "kvf_merge", "timeline_plan"):
         o = os.path.join(BUILD, name + ".o")
-        extra = ["-mllvm", "-amdgpu-kernarg-preload-count=10"] if name == "kvf_merge" else []
+        # kernel-argument preloading as the library's build has it
+        extra = ["-mllvm", "-amdgpu-kernarg-preload-count=" + ("10" if name == "kvf_merge" else "14")]
         subprocess.run([HIPCC] + FLAGS + extra + ["-I" + csrc, "-I" + os.path.join(ROOT, "include"), "-c",
                                                   os.path.join(csrc, name + ".hip"), "-o", o], check=True)
         objs.append(o)
